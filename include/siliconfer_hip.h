@@ -1,0 +1,129 @@
+/* siliconfer_hip.h — C ABI of the MI355X (gfx950) quantized-inference hot path.
+ *
+ * One shared library, libsiliconfer_hip.so, built from the HIP sources in siliconfer_amd/csrc.
+ * Conventions for every entry point:
+ *   - all data pointers are DEVICE memory owned by the caller;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); work is
+ *     enqueued and the call returns without synchronising;
+ *   - nothing allocates device memory; kernels that need scratch take a
+ *     caller-provided workspace whose size a *_workspace_bytes() call reports;
+ *   - return 0 on success, a negative SF_E* code otherwise; sf_last_error()
+ *     then holds a message for the calling thread. Shape errors reuse the
+ *     reference's message texts ("scales shape mismatch", "in_features must
+ *     be divisible by group_size", ...) from
+ *     /root/reference/siliconfer/kernels/neon/bindings.cpp:24-40.
+ *
+ * Weight format at the boundary is the reference's canonical one
+ * (siliconfer/kernels/neon/__init__.py:42-81, quant/primitives.py:332-349):
+ * packed uint8 [N, K/2], byte (i,j) = q[i,2j] | q[i,2j+1] << 4; symmetric codes
+ * are two's-complement nibbles, asymmetric codes unsigned. Scales are fp16
+ * [N, K/g]; zero-points are integral values 0..15 given as uint8 [N, K/g].
+ * sf_q4_repack turns that into the device blob every GEMV/GEMM call reads.
+ */
+#ifndef SILICONFER_HIP_H
+#define SILICONFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SF_ABI_VERSION 1
+
+/* return codes */
+#define SF_OK 0
+#define SF_EINVAL (-1)       /* bad shape / argument (reference: std::runtime_error) */
+#define SF_EUNSUPPORTED (-2) /* valid for the reference, outside this build's kernels */
+#define SF_EHIP (-3)         /* a HIP runtime call or launch failed */
+
+/* element types for activations, KV inputs, attention q/out and KV scales */
+#define SF_F32 0
+#define SF_F16 1
+#define SF_BF16 2
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *sf_last_error(void);
+
+/* SF_ABI_VERSION of the loaded library. */
+int sf_abi_version(void);
+
+/* 1 if `device` is a gfx950 (MI355X-class) device, 0 otherwise, <0 on error. */
+int sf_device_arch_ok(int device);
+
+/* ---- int4 weights: canonical -> device blob ----------------------------- */
+
+/* Bytes of the device blob for an N x K int4 matrix with group size g.
+ * Replaces the reference's packed-array allocation in pack_weights_sym/asym
+ * (siliconfer/kernels/neon/__init__.py:42-81); 0 if the shape is invalid. */
+size_t sf_q4_blob_bytes(int N, int K, int group_size, int has_zeros);
+
+/* Canonical (packed u8 [N,K/2], scales f16 [N,K/g], zeros u8 [N,K/g] or NULL)
+ * -> blob. has_zeros = (zeros != NULL) selects asymmetric codes. Same
+ * validation as check_gemv (bindings.cpp:24-40). group_size must be a
+ * multiple of 32 (SF_EUNSUPPORTED otherwise). */
+int sf_q4_repack(const uint8_t *packed, const void *scales_f16, const uint8_t *zeros_u8,
+                 int N, int K, int group_size, void *blob, size_t blob_bytes, void *stream);
+
+/* Blob -> canonical (inverse of sf_q4_repack; zeros_u8 may be NULL for sym). */
+int sf_q4_unpack(const void *blob, int N, int K, int group_size, int has_zeros,
+                 uint8_t *packed, void *scales_f16, uint8_t *zeros_u8, void *stream);
+
+/* ---- decode GEMV (batch 1..8) -------------------------------------------
+ * y[b, n] = sum_g s[n,g] * sum_{k in g} (q[n,k] - z[n,g]) x[b,k]   (z = 0 sym)
+ * Replaces q4_gemv_sym / q4_gemv_asym (bindings.cpp:45-93) and, through
+ * Q4Linear at T<=8 rows, q4_gemm_sym / q4_gemm_asym (bindings.cpp:98-150).
+ * x: [B, K] of x_dtype (SF_F16 or SF_BF16). Outputs: y [B, N] of y_dtype
+ * (SF_F16 / SF_BF16 / SF_F32), and/or y_f32 [B, N]; either may be NULL but
+ * not both. bias: NULL or [N] of bias_dtype (added before the store). fp32
+ * accumulation throughout. */
+int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
+               const void *bias, int bias_dtype, int B, int N, int K, int group_size,
+               int has_zeros, void *stream);
+
+/* ---- prefill GEMM (M rows) ------------------------------------------------
+ * Y[m, n] = X[m, :] . dequant(W)[n, :] for M rows; replaces q4_gemm_sym /
+ * q4_gemm_asym (bindings.cpp:98-150; q4_gemm.cpp:12-51). bf16/f16 MFMA on
+ * integer-valued int4 codes, fp32 per-(row, group) scale epilogue.
+ * workspace: sf_q4_gemm_workspace_bytes(...) bytes (may be 0 -> NULL ok). */
+size_t sf_q4_gemm_workspace_bytes(int M, int N, int K, int group_size);
+int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
+               const void *bias, int bias_dtype, int M, int N, int K, int group_size,
+               int has_zeros, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- int8 KV cache ----------------------------------------------------------
+ * Quantize T_new new tokens and write them at positions [T_off, T_off+T_new)
+ * of a preallocated cache. Replaces quantize_kv + the concatenation in
+ * QuantizedKVCache.update (siliconfer/model/kv_cache.py:49-63, 90-105).
+ * k_new/v_new: [B, KVH, T_new, D] of in_dtype, contiguous.
+ * codes: int8 [B, KVH, T_cap, D]; scales: [B, KVH, T_cap] of scale_dtype
+ * (SF_F16 or SF_F32). Per (b, h, t): s = max|x|/127 (1 if 0), computed in
+ * fp32; code = clip(rint(x/s), -128, 127); the stored scale is s rounded to
+ * scale_dtype. */
+int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_t *k_codes,
+                       void *k_scales, int8_t *v_codes, void *v_scales, int scale_dtype,
+                       int B, int KVH, int T_new, int T_off, int T_cap, int D, void *stream);
+
+/* ---- fused decode attention over the int8 cache ----------------------------
+ * out[b, h, :] = softmax(scale * q[b,h] . K[b, h/(H/KVH), :T]^T) V[...]
+ * with K = k_codes * k_scales per token (likewise V). Replaces
+ * fused_quantized_attention_decode (siliconfer/kernels/metal/q4_attention.py:
+ * 200-261). q: [B, H, D] of q_dtype; out: [B, H, D] of out_dtype. n_splits is
+ * the split-T count (the reference's n_tiles; <=0 picks a default). D <= 256
+ * (the reference's bound, q4_attention.py:78,227-228) and D % 8 == 0.
+ * workspace: sf_attn_workspace_bytes(B, H, D, n_splits) bytes. */
+size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
+int sf_attn_default_splits(int B, int KVH, int T);
+int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const void *k_scales,
+                        const int8_t *v_codes, const void *v_scales, int scale_dtype, void *out,
+                        int out_dtype, void *workspace, size_t workspace_bytes, int B, int H,
+                        int KVH, int T, int T_cap, int D, float scale, int n_splits,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SILICONFER_HIP_H */

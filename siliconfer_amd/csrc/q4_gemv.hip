@@ -1,0 +1,59 @@
+// q4_gemv.hip — C entry point of the int4 decode GEMV (kernels in q4_gemv_kernel.h).
+#include "q4_gemv_kernel.h"
+
+namespace sf_gemv {
+extern template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
+extern template void launch_x<SF_BF16>(const GemvPlan &, const GemvArgs &);
+extern template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
+}  // namespace sf_gemv
+
+using namespace sf_gemv;
+
+extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
+                          float *y_f32, const void *bias, int bias_dtype, int B, int N, int K,
+                          int group_size, int has_zeros, void *stream) {
+  SF_REQUIRE(N > 0 && K > 0 && group_size > 0, SF_EINVAL, "invalid shape N=%d K=%d group_size=%d",
+             N, K, group_size);
+  SF_REQUIRE(K % group_size == 0, SF_EINVAL, "in_features must be divisible by group_size");
+  SF_REQUIRE(group_size % 32 == 0, SF_EUNSUPPORTED,
+             "group_size=%d: this build's kernels need a multiple of 32", group_size);
+  SF_REQUIRE(B >= 1 && B <= 8, SF_EINVAL, "GEMV batch must be 1..8 (got %d)", B);
+  SF_REQUIRE(blob && x && (y || y_f32), SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(x_dtype == SF_F16 || x_dtype == SF_BF16 || x_dtype == SF_F32, SF_EINVAL,
+             "bad activation dtype %d", x_dtype);
+  SF_REQUIRE(y_dtype == SF_F16 || y_dtype == SF_BF16 || y_dtype == SF_F32, SF_EINVAL,
+             "bad output dtype %d", y_dtype);
+  SF_REQUIRE(!bias || bias_dtype == SF_F16 || bias_dtype == SF_BF16 || bias_dtype == SF_F32,
+             SF_EINVAL, "bad bias dtype %d", bias_dtype);
+  SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)x & 15) == 0, SF_EINVAL,
+             "blob must be 256-byte aligned and x 16-byte aligned");
+  BlobLayout L;
+  sf_blob_layout(N, K, group_size, has_zeros, &L);
+  GemvPlan pl;
+  int rc = plan_gemv(B, N, K, group_size, &pl);
+  if (rc) return rc;
+  const uint8_t *w = (const uint8_t *)blob;
+  const f16 *st = (const f16 *)(w + L.s_off);
+  const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
+  GemvArgs args{w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, L.G, has_zeros != 0,
+                (hipStream_t)stream};
+  if (x_dtype == SF_F16) {
+    launch_x<SF_F16>(pl, args);
+  } else if (x_dtype == SF_BF16) {
+    launch_x<SF_BF16>(pl, args);
+  } else {
+    // fp32 activations run in slices of <= 2 batch rows
+    const size_t ysz = y_dtype == SF_F32 ? 4 : 2;
+    for (int b0 = 0; b0 < B; b0 += 2) {
+      GemvArgs sl = args;
+      sl.B = B - b0 < 2 ? B - b0 : 2;
+      sl.x = (const float *)x + (size_t)b0 * K;
+      if (y) sl.y = (char *)y + (size_t)b0 * N * ysz;
+      if (y_f32) sl.y32 = y_f32 + (size_t)b0 * N;
+      GemvPlan p2;
+      plan_gemv(sl.B, N, K, group_size, &p2);
+      launch_x<SF_F32>(p2, sl);
+    }
+  }
+  return sf_check_launch("sf_q4_gemv");
+}

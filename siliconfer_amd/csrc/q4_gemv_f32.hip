@@ -1,0 +1,7 @@
+// q4_gemv_f32.hip — GEMV instantiations for f32 activations (kernel in q4_gemv_kernel.h;
+// one translation unit per activation type keeps the build parallel).
+#include "q4_gemv_kernel.h"
+
+namespace sf_gemv {
+template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
+}  // namespace sf_gemv

@@ -1,0 +1,116 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/siliconfer_hip.h declares, sizes are computed on the host, and argument
+validation rejects bad shapes with the reference's messages
+(siliconfer/kernels/neon/bindings.cpp:24-40) before touching the device.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from siliconfer_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "siliconfer_hip.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_surface():
+    names = declared_functions()
+    for n in ("sf_q4_repack", "sf_q4_gemv", "sf_q4_gemm", "sf_kv_quant_append",
+              "sf_attn_decode_i8kv", "sf_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    assert set(declared_functions()) == set(_lib.exported_symbols())
+
+
+def test_abi_version():
+    assert _lib.load().sf_abi_version() == 1
+
+
+def test_blob_bytes_layout():
+    lib = _lib.load()
+    # sym 4096x4096 g128: weights 8 MiB, scales 512 octets x 32 groups x 8 x 2 B
+    assert lib.sf_q4_blob_bytes(4096, 4096, 128, 0) == 8388608 + 512 * 32 * 16
+    # asym adds 4 bytes per (octet, group) after a 256-byte aligned offset
+    nb = lib.sf_q4_blob_bytes(4864, 896, 64, 1)
+    w = 4864 * 448
+    s_off = (w + 255) // 256 * 256
+    z_off = (s_off + 608 * 14 * 16 + 255) // 256 * 256
+    assert nb == z_off + 608 * 14 * 4
+    assert lib.sf_q4_blob_bytes(10, 100, 64, 0) == 0      # K % g != 0
+    assert lib.sf_q4_blob_bytes(0, 128, 64, 0) == 0
+
+
+@pytest.mark.parametrize("K,g,code,msg", [
+    (100, 64, -1, "in_features must be divisible by group_size"),
+    (96, 48, -2, "multiple of 32"),
+])
+def test_repack_rejects_bad_shapes(K, g, code, msg):
+    lib = _lib.load()
+    rc = lib.sf_q4_repack(None, None, None, 8, K, g, None, 0, None)
+    assert rc == code
+    assert msg in _lib.last_error()
+
+
+def test_gemv_rejects_batch_and_dtype():
+    lib = _lib.load()
+    rc = lib.sf_q4_gemv(None, None, 1, None, 1, None, None, 0, 9, 16, 128, 64, 0, None)
+    assert rc == -1 and "batch must be 1..8" in _lib.last_error()
+    rc = lib.sf_q4_gemv(None, None, 1, None, 1, None, None, 0, 1, 16, 100, 64, 0, None)
+    assert rc == -1 and "in_features must be divisible by group_size" in _lib.last_error()
+
+
+def test_gemm_workspace_and_validation():
+    lib = _lib.load()
+    assert lib.sf_q4_gemm_workspace_bytes(512, 4864, 896, 64) == 0      # 152 tiles: no split
+    assert lib.sf_q4_gemm_workspace_bytes(512, 896, 4864, 64) > 0       # 28 tiles: split K
+    rc = lib.sf_q4_gemm(None, None, 2, None, 2, None, None, 0, 4, 16, 96, 48, 0, None, 0, None)
+    assert rc == -2
+
+
+def test_attention_validation_and_sizes():
+    lib = _lib.load()
+    assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == 14 * 256 * 64 * 4 + 14 * 256 * 2 * 4
+    rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
+                                 1, 14, 2, 16, 16, 512, 0.1, 1, None)
+    assert rc == -1 and "exceeds kernel's compile-time max 256" in _lib.last_error()
+    rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
+                                 1, 14, 3, 16, 16, 64, 0.1, 1, None)
+    assert rc == -1 and "not a multiple" in _lib.last_error()
+    assert lib.sf_attn_default_splits(1, 2, 16384) == 256
+    assert lib.sf_attn_default_splits(1, 2, 100) == 2
+
+
+def test_kv_append_validation():
+    lib = _lib.load()
+    rc = lib.sf_kv_quant_append(None, None, 1, None, None, None, None, 1, 1, 2, 4, 10, 12, 64, None)
+    assert rc == -1 and "overflow" in _lib.last_error()
+
+
+def test_python_layer_raises_without_device():
+    """No CPU fallback: on a host without a GPU the product refuses to compute."""
+    import numpy as np
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from siliconfer_amd import kernels as K
+
+    assert K.HIP_AVAILABLE is False
+    W = np.random.default_rng(0).normal(0, 1, (16, 64)).astype(np.float32)
+    pk, s = K.pack_weights_sym(W, 64)
+    with pytest.raises(RuntimeError):
+        K.gemv_sym(pk, s, np.ones(64, np.float32), 64)

@@ -1,0 +1,102 @@
+"""GPU parity of the int4 prefill GEMM (MFMA) against the oracle, through the C
+ABI (sf_q4_gemm). Bar: 1e-3 relative (oracle.linear.assert_close).
+Reference tests restated: tests/test_kernel.py:136-151, 181-210.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import linear, primitives as P
+from siliconfer_amd.kernels import Q4Weight
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def s16(s):
+    return np.asarray(s, np.float32).astype(np.float16).astype(np.float64)
+
+
+def laplace_outliers(rng, shape, b=0.015):
+    W = rng.laplace(0, b, shape).astype(np.float32)
+    n_out = max(1, round(W.size / 1e6))
+    idx = rng.choice(W.size, n_out, replace=False)
+    W.reshape(-1)[idx] = (40 * b * np.sqrt(2) * rng.choice([-1, 1], n_out)).astype(np.float32)
+    return W
+
+
+def gemm_dev(dev, pk, s, z, X, g, xdtype, out_dtype=torch.float32, bias=None):
+    w = Q4Weight(pk, s, z, g, device=dev)
+    xt = torch.as_tensor(X, dtype=torch.float32).to(dev).to(xdtype).contiguous()
+    bt = None if bias is None else torch.as_tensor(bias).to(dev)
+    y = w.matmul(xt, out_dtype=out_dtype, bias=bt)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy().astype(np.float64), xt.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("N,K", [(4864, 896), (896, 4864)])
+def test_config2_asym_prefill(dev, N, K):
+    """X bf16 [512, K] ~ N(0,1); W ~ Laplace(0, 0.015) with 40-sigma
+    outliers; asym g=64, fp16 scales, uint4 zero-points. Up/gate and down shapes."""
+    rng = np.random.default_rng(1)
+    W = laplace_outliers(rng, (N, K))
+    pk, s, z = P.pack_weights_asym(W, 64)
+    X = rng.normal(0, 1, (512, K)).astype(np.float32)
+    y, xk = gemm_dev(dev, pk, s, z, X, 64, torch.bfloat16)
+    linear.assert_close(y, linear.gemm(pk, s16(s), xk, 64, zeros=z), TOL, f"config2 [{N},{K}]")
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K,g", [(33, 100, 256, 64), (200, 257, 512, 128), (130, 640, 96, 32)])
+def test_gemm_shapes_and_dtypes_sym(dev, xdtype, M, N, K, g):
+    rng = np.random.default_rng(M + N + K)
+    W = rng.normal(0, 1, (N, K)).astype(np.float32)
+    pk, s = P.pack_weights_sym(W, g)
+    X = rng.normal(0, 1, (M, K)).astype(np.float32)
+    y, xk = gemm_dev(dev, pk, s, None, X, g, xdtype)
+    linear.assert_close(y, linear.gemm(pk, s16(s), xk, g), TOL, f"{M}x{N}x{K} {xdtype}")
+
+
+def test_gemm_asym_matches_fake_quant_matmul(dev):
+    """tests/test_kernel.py:198-210 (T = 8 goes to the GEMV; 64 to the GEMM)."""
+    rng = np.random.default_rng(3)
+    W = rng.normal(0, 1, (32, 128)).astype(np.float32)
+    pk, s, z = P.pack_weights_asym(W, 128)
+    Wq = P.dequant_packed(pk, s16(s), z, 128)
+    for T in (8, 64):
+        X = rng.normal(0, 1, (T, 128)).astype(np.float32)
+        y, xk = gemm_dev(dev, pk, s, z, X, 128, torch.float32)
+        linear.assert_close(y, xk @ Wq.T, TOL, f"T={T}")
+
+
+@pytest.mark.parametrize("asym", [False, True])
+def test_gemm_equals_gemv_loop(dev, asym):
+    """tests/test_kernel.py:136-151, 181-195: rows of the GEMM equal single-row GEMVs."""
+    rng = np.random.default_rng(99)
+    W = rng.normal(0, 1, (64, 128)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, 64)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, 64), None
+    w = Q4Weight(pk, s, z, 64, device=dev)
+    X = torch.as_tensor(rng.normal(0, 1, (32, 128)).astype(np.float16)).to(dev)
+    Y = w.matmul(X, out_dtype=torch.float32)
+    rows = torch.cat([w.matmul(X[t:t + 1].contiguous(), out_dtype=torch.float32) for t in range(32)])
+    linear.assert_close(Y.cpu().numpy(), rows.cpu().numpy(), 1e-5, "gemm vs gemv loop")
+
+
+def test_gemm_bias_and_split_k_determinism(dev):
+    rng = np.random.default_rng(12)
+    N, K = 896, 4864                       # 28 output tiles at M=512: split-K path
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    pk, s = P.pack_weights_sym(W, 64)
+    X = rng.normal(0, 1, (512, K)).astype(np.float32)
+    y, xk = gemm_dev(dev, pk, s, None, X, 64, torch.bfloat16, bias=b)
+    linear.assert_close(y, linear.gemm(pk, s16(s), xk, 64) + b, TOL, "split-K + bias")
+    w = Q4Weight(pk, s, None, 64, device=dev)
+    xt = torch.as_tensor(X).to(dev).to(torch.bfloat16)
+    first = w.matmul(xt, out_dtype=torch.float32).clone()
+    for _ in range(5):
+        assert torch.equal(w.matmul(xt, out_dtype=torch.float32), first)

@@ -1,0 +1,202 @@
+"""GPU parity of the int4 decode GEMV (B = 1..8) against the oracle and the
+reference's golden vectors, through the C ABI (sf_q4_repack / sf_q4_gemv).
+
+Bar: fp32-accumulated output within 1e-3 relative —
+norm-relative max error AND elementwise |y - y*| <= 1e-3 |y*| + 1e-3 max|y*|
+(oracle.linear.assert_close). The oracle uses exactly the values the kernel is
+given: fp16-rounded scales, and activations as rounded to the kernel's dtype.
+Reference tests restated: tests/test_kernel.py:38-129, 167-178.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_cases, load_golden
+from oracle import linear, primitives as P
+from siliconfer_amd.kernels import Q4Weight
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def run_gemv(dev, packed, scales, zeros, x, g, xdtype=torch.float16, bias=None,
+             out_dtype=torch.float16):
+    """-> (y_f32 numpy [B, N], y in out_dtype as numpy float64, x as the kernel saw it)."""
+    w = Q4Weight(packed, scales, zeros, g, device=dev)
+    xt = torch.as_tensor(np.atleast_2d(x), dtype=torch.float32).to(dev).to(xdtype).contiguous()
+    B, N = xt.shape[0], packed.shape[0]
+    y32 = torch.empty((B, N), dtype=torch.float32, device=dev)
+    y = torch.empty((B, N), dtype=out_dtype, device=dev)
+    bt = None if bias is None else torch.as_tensor(bias).to(dev)
+    w.matmul(xt, bias=bt, out=y, out_f32=y32)
+    torch.cuda.synchronize()
+    return y32.cpu().numpy(), y.float().cpu().numpy().astype(np.float64), xt.float().cpu().numpy()
+
+
+def s16(s):
+    return np.asarray(s, np.float32).astype(np.float16).astype(np.float64)
+
+
+@pytest.mark.parametrize("name", golden_cases("gemv_"))
+def test_golden_reference_vectors(dev, name):
+    c = load_golden(name)
+    g = int(c["g"])
+    y32, _, _ = run_gemv(dev, c["packed"], c["scales"], None, c["x"], g)
+    linear.assert_close(y32[0], c["y_ref16"], TOL, name)
+
+
+@pytest.mark.parametrize("name", golden_cases("gemm_"))
+def test_golden_reference_gemm_vectors(dev, name):
+    """T = 4 goes through the GEMV (<= 8 rows), T = 32 through the MFMA GEMM."""
+    c = load_golden(name)
+    g = int(c["g"])
+    w = Q4Weight(c["packed"], c["scales"], None, g, device=dev)
+    X = torch.as_tensor(c["x"]).to(dev)
+    for dt in (torch.float16, torch.float32):
+        Y = w.matmul(X.to(dt).contiguous(), out_dtype=torch.float32)
+        linear.assert_close(Y.cpu().numpy(), c["y_ref16"], TOL, f"{name}/{dt}")
+
+
+def test_config1_decode_gemv(dev):
+    """W [4864, 896] ~ N(0, 0.02), RTN sym g=64, x fp16 [1, 896]."""
+    rng = np.random.default_rng(0)
+    W = rng.normal(0, 0.02, (4864, 896)).astype(np.float32)
+    x = rng.normal(0, 1, (1, 896)).astype(np.float16)
+    pk, s = P.pack_weights_sym(W, 64)
+    y32, y16, xk = run_gemv(dev, pk, s, None, x, 64)
+    ref = linear.gemv(pk, s16(s), xk, 64)
+    linear.assert_close(y32, ref, TOL, "config1 f32")
+    linear.assert_close(y16, ref, TOL, "config1 fp16 out")
+
+
+@pytest.fixture(scope="module")
+def config3_cases():
+    out = []
+    for i, (N, K) in enumerate([(4096, 4096), (11008, 4096), (4096, 11008)]):
+        rng = np.random.default_rng(2 + i)
+        W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        x = rng.normal(0, 1, (8, K)).astype(np.float16)
+        pk, s = P.pack_weights_sym(W, 128)
+        ref = linear.gemv(pk, s16(s), x.astype(np.float64), 128)   # [8, N]
+        out.append((N, K, pk, s, x, ref))
+    return out
+
+
+@pytest.mark.parametrize("shape_idx", [0, 1, 2])
+def test_config3_7b_shapes_all_batches(dev, config3_cases, shape_idx):
+    """7B shapes, sym g=128, batch 1, 2, 4, 8 (plus 3, 5, 6, 7)."""
+    N, K, pk, s, x, ref = config3_cases[shape_idx]
+    w = Q4Weight(pk, s, None, 128, device=dev)
+    xt = torch.as_tensor(x).to(dev)
+    for B in range(1, 9):
+        y32 = torch.empty((B, N), dtype=torch.float32, device=dev)
+        w.matmul(xt[:B].contiguous(), out_f32=y32)
+        linear.assert_close(y32.cpu().numpy(), ref[:B], TOL, f"[{N},{K}] B={B}")
+
+
+def _laplace_with_outliers(rng, shape, b=0.015):
+    W = rng.laplace(0, b, shape).astype(np.float32)
+    n_out = max(1, round(W.size / 1e6))
+    idx = rng.choice(W.size, n_out, replace=False)
+    W.reshape(-1)[idx] = (40 * b * np.sqrt(2) * rng.choice([-1, 1], n_out)).astype(np.float32)
+    return W
+
+
+@pytest.mark.parametrize("N,K", [(4864, 896), (896, 4864)])
+def test_asym_gemv_config2_weights(dev, N, K):
+    """Asymmetric (HQQ-style) codes with zero-points, the config-2 weights, B = 1..8."""
+    rng = np.random.default_rng(1)
+    W = _laplace_with_outliers(rng, (N, K))
+    pk, s, z = P.pack_weights_asym(W, 64)
+    x = rng.normal(0, 1, (8, K)).astype(np.float16)
+    ref = linear.gemv(pk, s16(s), x.astype(np.float64), 64, zeros=z)
+    w = Q4Weight(pk, s, z, 64, device=dev)
+    xt = torch.as_tensor(x).to(dev)
+    for B in (1, 2, 3, 8):
+        y = w.matmul(xt[:B].contiguous(), out_dtype=torch.float32)
+        linear.assert_close(y.cpu().numpy(), ref[:B], TOL, f"asym [{N},{K}] B={B}")
+
+
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("asym", [False, True])
+def test_bf16_and_f32_activations(dev, xdtype, asym):
+    rng = np.random.default_rng(21)
+    N, K = 1000, 2048
+    W = rng.normal(0.01 if asym else 0, 0.02, (N, K)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, 128)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, 128), None
+    x = rng.normal(0, 3, (5, K)).astype(np.float32)
+    for B in (1, 2, 5):
+        y32, _, xk = run_gemv(dev, pk, s, z, x[:B], 128, xdtype=xdtype)
+        ref = linear.gemv(pk, s16(s), xk.astype(np.float64), 128, zeros=z)
+        linear.assert_close(y32, ref, TOL, f"{xdtype} asym={asym} B={B}")
+
+
+@pytest.mark.parametrize("N,K,g", [
+    (1, 128, 128),      # single row (test_kernel.py:121-129)
+    (13, 128, 64),      # rows not a multiple of 8; 4 lanes per row
+    (77, 1024, 32),     # 32 lanes per row, group 32
+    (130, 2048, 64),    # one full wave per row
+    (129, 4864, 64),    # 3 waves per row (down projection width)
+    (33, 16384, 256),   # widest supported row: 8 waves
+])
+def test_edge_shapes(dev, N, K, g):
+    rng = np.random.default_rng(N * 7 + K)
+    W = rng.normal(0, 1, (N, K)).astype(np.float32)
+    pk, s = P.pack_weights_sym(W, g)
+    x = rng.normal(0, 1, (3, K)).astype(np.float16)
+    for B in (1, 3):
+        y32, _, xk = run_gemv(dev, pk, s, None, x[:B], g)
+        linear.assert_close(y32, linear.gemv(pk, s16(s), xk, g), TOL, f"N={N} K={K} B={B}")
+
+
+def test_zero_input_gives_zero(dev):
+    rng = np.random.default_rng(0)
+    pk, s = P.pack_weights_sym(rng.normal(0, 1, (32, 128)).astype(np.float32), 128)
+    y32, _, _ = run_gemv(dev, pk, s, None, np.zeros((1, 128), np.float32), 128)
+    assert np.all(y32 == 0)
+
+
+def test_bias_and_output_dtypes(dev):
+    rng = np.random.default_rng(4)
+    W = rng.normal(0, 1, (64, 256)).astype(np.float32)
+    b = rng.normal(0, 0.1, 64).astype(np.float32)
+    pk, s = P.pack_weights_sym(W, 64)
+    x = rng.normal(0, 1, (2, 256)).astype(np.float16)
+    ref = linear.gemv(pk, s16(s), x.astype(np.float64), 64) + b
+    for od in (torch.float16, torch.bfloat16, torch.float32):
+        y32, y, _ = run_gemv(dev, pk, s, None, x, 64, bias=b, out_dtype=od)
+        linear.assert_close(y32, ref, TOL, "bias f32")
+        rounding = {torch.float16: 2 ** -11, torch.bfloat16: 2 ** -8, torch.float32: 1e-7}[od]
+        linear.assert_close(y, ref, TOL + rounding, f"bias {od}")
+
+
+def test_repeated_launches_bitwise_identical(dev):
+    """The reduction order is fixed: repeated calls give identical bits
+    (the reference's race check, tests/test_metal_attention.py:87-103)."""
+    rng = np.random.default_rng(7)
+    pk, s = P.pack_weights_sym(rng.normal(0, 0.02, (4096, 4096)).astype(np.float32), 128)
+    w = Q4Weight(pk, s, None, 128, device=dev)
+    x = torch.as_tensor(rng.normal(0, 1, (4, 4096)).astype(np.float16)).to(dev)
+    first = w.matmul(x, out_dtype=torch.float32).clone()
+    for _ in range(10):
+        assert torch.equal(w.matmul(x, out_dtype=torch.float32), first)
+
+
+@pytest.mark.parametrize("asym", [False, True])
+def test_repack_round_trip_bit_exact(dev, asym):
+    rng = np.random.default_rng(5)
+    W = rng.normal(0, 1, (37, 384)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, 128)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, 128), None
+    w = Q4Weight(pk, s, z, 128, device=dev)
+    pk2, s2, z2 = w.canonical()
+    np.testing.assert_array_equal(pk2.cpu().numpy(), pk)
+    np.testing.assert_array_equal(s2.cpu().numpy(), s.astype(np.float16))
+    if asym:
+        np.testing.assert_array_equal(z2.cpu().numpy(), z.astype(np.uint8))
