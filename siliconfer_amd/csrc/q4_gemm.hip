@@ -13,8 +13,8 @@
 // into LDS as these two bf16 tiles, and every wave runs
 // v_mfma_f32_32x32x16_bf16 on X*W_hi + X*W_lo. bf16 activations are exact
 // operands; fp16 / fp32 activations are split the same way into bf16 hi + lo
-// (fp16 exactly, fp32 to ~16 bits) and the three products hi*hi, hi*lo, lo*hi
-// are accumulated.
+// (fp16 exactly, fp32 to ~16 bits) and all four products are accumulated, so
+// fp16 activations give exact products like the bf16 ones.
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup (2 x 2 waves, each
 // 64 x 64 = 2 x 2 MFMA 32x32 tiles), K steps of 64 staged through padded LDS
@@ -56,12 +56,12 @@ __device__ __forceinline__ void load_x(XRegs<XDT> &r, const void *X, int M, int 
 
 // Split 2 fp32 values into (hi pair, lo pair) of bf16: hi = truncation, lo = rest.
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-  const uint32_t ua = __builtin_bit_cast(uint32_t, a) & 0xFFFF0000u;
-  const uint32_t ub = __builtin_bit_cast(uint32_t, b) & 0xFFFF0000u;
-  const float ra = a - __builtin_bit_cast(float, ua);
-  const float rb = b - __builtin_bit_cast(float, ub);
+  const uint32_t ua = sf_bitcast<uint32_t>(a) & 0xFFFF0000u;
+  const uint32_t ub = sf_bitcast<uint32_t>(b) & 0xFFFF0000u;
+  const float ra = a - sf_bitcast<float>(ua);
+  const float rb = b - sf_bitcast<float>(ub);
   hi = hi_pair(ua, ub);
-  lo = hi_pair(__builtin_bit_cast(uint32_t, ra), __builtin_bit_cast(uint32_t, rb));
+  lo = hi_pair(sf_bitcast<uint32_t>(ra), sf_bitcast<uint32_t>(rb));
 }
 
 // Write the thread's 32 activations to the LDS tiles (hi only for bf16).
@@ -80,13 +80,13 @@ __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, ui
       if constexpr (XDT == SF_F16) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const half2_t h = __builtin_bit_cast(half2_t, r.v[i][j]);
+          const half2_t h = sf_bitcast<half2_t>(r.v[i][j]);
           f[2 * j] = (float)h.x;
           f[2 * j + 1] = (float)h.y;
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = __builtin_bit_cast(float, r.v[2 * i + j / 4][j % 4]);
+        for (int j = 0; j < 8; ++j) f[j] = sf_bitcast<float>(r.v[2 * i + j / 4][j % 4]);
       }
       u32x4 h4, l4;
 #pragma unroll
@@ -225,8 +225,10 @@ k_q4_gemm(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
         for (int j = 0; j < 2; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-          if constexpr (XSPLIT)
+          if constexpr (XSPLIT) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bl[j], acc[i][j], 0, 0, 0);
+          }
         }
     }
   }

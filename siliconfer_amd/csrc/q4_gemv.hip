@@ -30,7 +30,7 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
   BlobLayout L;
   sf_blob_layout(N, K, group_size, has_zeros, &L);
   GemvPlan pl;
-  int rc = plan_gemv(B, N, K, group_size, &pl);
+  int rc = plan_gemv(B, N, K, group_size, x_dtype, &pl);
   if (rc) return rc;
   const uint8_t *w = (const uint8_t *)blob;
   const f16 *st = (const f16 *)(w + L.s_off);
@@ -51,7 +51,7 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
       if (y) sl.y = (char *)y + (size_t)b0 * N * ysz;
       if (y_f32) sl.y32 = y_f32 + (size_t)b0 * N;
       GemvPlan p2;
-      plan_gemv(sl.B, N, K, group_size, &p2);
+      plan_gemv(sl.B, N, K, group_size, x_dtype, &p2);
       launch_x<SF_F32>(p2, sl);
     }
   }

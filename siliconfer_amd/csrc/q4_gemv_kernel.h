@@ -32,75 +32,117 @@
 //    reduce-scatter inside the wave (each step halves the values a lane holds),
 //    then across the rowset's waves through LDS when P > 64.
 #pragma once
+#include <stdlib.h>
+
 #include "sf_common.h"
 
 namespace sf_gemv {
 
+// Scales of R consecutive rows (row0 % R == 0) of one group from the tiled
+// [octet][group][8] fp16 array; cell points at the (row0 / 8, group) octet.
 template <int R>
-struct ScaleLoad;
-
-template <>
-struct ScaleLoad<4> {
-  __device__ __forceinline__ static void load(const f16 *tile_base, int row0, int N, float (&s)[4]) {
-    u32x2 v = {0u, 0u};
-    if (row0 < N) v = *(const u32x2 *)(tile_base + (row0 & 7));
-    half2_t a = __builtin_bit_cast(half2_t, v.x), b = __builtin_bit_cast(half2_t, v.y);
-    s[0] = (float)a.x; s[1] = (float)a.y; s[2] = (float)b.x; s[3] = (float)b.y;
-  }
-};
-
-template <>
-struct ScaleLoad<8> {
-  __device__ __forceinline__ static void load(const f16 *tile_base, int row0, int N, float (&s)[8]) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (row0 < N) v = *(const u32x4 *)tile_base;
+__device__ __forceinline__ void load_scales(const f16 *cell, size_t octet_stride, int row0, int N,
+                                            float (&s)[R]) {
+  if constexpr (R >= 8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      half2_t h = __builtin_bit_cast(half2_t, v[i]);
-      s[2 * i] = (float)h.x;
-      s[2 * i + 1] = (float)h.y;
+    for (int o = 0; o < R / 8; ++o) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row0 + 8 * o < N) v = *(const u32x4 *)(cell + (size_t)o * octet_stride);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half2_t h = sf_bitcast<half2_t>(v[i]);
+        s[8 * o + 2 * i] = (float)h.x;
+        s[8 * o + 2 * i + 1] = (float)h.y;
+      }
+    }
+  } else if constexpr (R == 4) {
+    u32x2 v = {0u, 0u};
+    if (row0 < N) v = *(const u32x2 *)(cell + (row0 & 7));
+    const half2_t a = sf_bitcast<half2_t>(v.x), b = sf_bitcast<half2_t>(v.y);
+    s[0] = (float)a.x; s[1] = (float)a.y; s[2] = (float)b.x; s[3] = (float)b.y;
+  } else {
+    uint32_t v = 0u;
+    if (row0 < N) v = *(const uint32_t *)(cell + (row0 & 7));
+    const half2_t a = sf_bitcast<half2_t>(v);
+    s[0] = (float)a.x; s[1] = (float)a.y;
+  }
+}
+
+// Zero-point nibbles of R consecutive rows of one group (row r at bits 4r).
+template <int R>
+__device__ __forceinline__ uint64_t load_zeros(const uint8_t *cell, size_t octet_stride, int row0, int N) {
+  if (row0 >= N) return 0u;
+  if constexpr (R == 16) {
+    const uint64_t lo = *(const uint32_t *)cell;
+    const uint64_t hi = row0 + 8 < N ? *(const uint32_t *)(cell + octet_stride) : 0u;
+    return lo | (hi << 32);
+  } else if constexpr (R == 8) {
+    return *(const uint32_t *)cell;
+  } else if constexpr (R == 4) {
+    return *(const uint16_t *)(cell + ((row0 & 7) >> 1));
+  } else {
+    return *(const uint8_t *)(cell + ((row0 & 7) >> 1));
+  }
+}
+
+// (a & m) | c in one instruction (the compiler splits it in two when both
+// constants would need literal operands).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
+// Value of the butterfly partner at lane distance OFF. OFF <= 8 uses DPP
+// (quad permutes and the 8-/16-lane mirrors: the partner always has the
+// opposite bit OFF and the same higher bits, which is all a butterfly step
+// needs); larger distances go through ds_bpermute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int OFF>
+__device__ __forceinline__ float partner(float v) {
+  if constexpr (OFF == 1) return dpp_f<0xB1>(v);        // quad_perm [1,0,3,2]
+  else if constexpr (OFF == 2) return dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  else if constexpr (OFF == 4) return dpp_f<0x141>(v);  // row_half_mirror: i <-> 7-i
+  else if constexpr (OFF == 8) return dpp_f<0x140>(v);  // row_mirror: i <-> 15-i
+  else return __shfl_xor(v, OFF, 64);
+}
+
+// Butterfly reduce-scatter of v[b][0..R) across a Q-lane group, starting at
+// lane distance OFF = Q/2 with RC values per lane. Each step at distance OFF
+// keeps the half of the values selected by the lane's own bit OFF and adds the
+// partner's same half; once one value is left the remaining steps are plain
+// sums. Afterwards lane p holds, in v[b][0..R>>S), the group sums of rows
+// (p >> (log2 Q - S)) * (R >> S) + j, S = min(log2 R, log2 Q).
+template <int B, int R, int OFF, int RC>
+__device__ __forceinline__ void butterfly(float (&v)[B][R], int p) {
+  if constexpr (OFF >= 1) {
+    if constexpr (RC > 1) {
+      constexpr int H = RC / 2;
+      const bool up = (p & OFF) != 0;
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+          const float lo = v[b][j], hi = v[b][j + H];
+          const float send = up ? lo : hi;
+          const float keep = up ? hi : lo;
+          v[b][j] = keep + partner<OFF>(send);
+        }
+      butterfly<B, R, OFF / 2, H>(v, p);
+    } else {
+#pragma unroll
+      for (int b = 0; b < B; ++b) v[b][0] += partner<OFF>(v[b][0]);
+      butterfly<B, R, OFF / 2, 1>(v, p);
     }
   }
-};
-
-// Zero-points of R rows (R = 4 or 8) of one group as nibbles in a u32.
-template <int R>
-__device__ __forceinline__ uint32_t load_zeros(const uint8_t *cell, int row0, int N) {
-  if (row0 >= N) return 0u;
-  if constexpr (R == 8) return *(const uint32_t *)cell;
-  else return (uint32_t)(*(const uint16_t *)(cell + ((row0 & 7) >> 1)));
 }
 
-// Butterfly reduce-scatter of v[b][0..R) across a Q-lane group (Q = 32 or 64).
-// Afterwards lane p holds, in v[b][0..R>>S), the rowset sums of rows
-// (p >> (LQ-S)) * (R>>S) + j, where S = min(log2 R, log2 Q).
-template <int B, int R, int Q>
-__device__ __forceinline__ void rowset_reduce(float (&v)[B][R], int p) {
-  constexpr int LQ = Q == 64 ? 6 : 5;
-  constexpr int LR = R == 8 ? 3 : 2;
-  constexpr int S = LR < LQ ? LR : LQ;
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const int off = Q >> (s + 1);
-    const bool up = (p & off) != 0;
-    const int H = R >> (s + 1);
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int j = 0; j < H; ++j) {
-        const float lo = v[b][j], hi = v[b][j + H];
-        const float send = up ? lo : hi;
-        const float keep = up ? hi : lo;
-        v[b][j] = keep + sf_shfl_xor(send, off);
-      }
-  }
-#pragma unroll
-  for (int off = Q >> (S + 1); off >= 1; off >>= 1)
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int j = 0; j < (R >> S); ++j) v[b][j] += sf_shfl_xor(v[b][j], off);
-}
+template <int V>
+constexpr int clog2() { return V <= 1 ? 0 : 1 + clog2<V / 2>(); }
 
 __device__ __forceinline__ void store_out(void *y, int ydt, float *y32, const void *bias, int bdt,
                                           size_t idx, int row, float v) {
@@ -130,8 +172,8 @@ struct Act<SF_F16> {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const u32x4 v = xq[q4];
-      const half2_t a = __builtin_bit_cast(half2_t, v.x), b = __builtin_bit_cast(half2_t, v.y);
-      const half2_t c = __builtin_bit_cast(half2_t, v.z), d = __builtin_bit_cast(half2_t, v.w);
+      const half2_t a = sf_bitcast<half2_t>(v.x), b = sf_bitcast<half2_t>(v.y);
+      const half2_t c = sf_bitcast<half2_t>(v.z), d = sf_bitcast<half2_t>(v.w);
       p[4 * q4 + 0] = half2_t{a.x, c.x};
       p[4 * q4 + 1] = half2_t{a.y, c.y};
       p[4 * q4 + 2] = half2_t{b.x, d.x};
@@ -153,13 +195,13 @@ struct Act<SF_BF16> {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const u32x4 v = xq[q4];
-      p[4 * q4 + 0] = __builtin_bit_cast(bf16x2_t, pair_lo_lo(v.x, v.z));
-      p[4 * q4 + 1] = __builtin_bit_cast(bf16x2_t, pair_hi_hi(v.x, v.z));
-      p[4 * q4 + 2] = __builtin_bit_cast(bf16x2_t, pair_lo_lo(v.y, v.w));
-      p[4 * q4 + 3] = __builtin_bit_cast(bf16x2_t, pair_hi_hi(v.y, v.w));
+      p[4 * q4 + 0] = sf_bitcast<bf16x2_t>(pair_lo_lo(v.x, v.z));
+      p[4 * q4 + 1] = sf_bitcast<bf16x2_t>(pair_hi_hi(v.x, v.z));
+      p[4 * q4 + 2] = sf_bitcast<bf16x2_t>(pair_lo_lo(v.y, v.w));
+      p[4 * q4 + 3] = sf_bitcast<bf16x2_t>(pair_hi_hi(v.y, v.w));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        sum += __builtin_bit_cast(float, v[i] << 16) + __builtin_bit_cast(float, v[i] & 0xFFFF0000u);
+        sum += sf_bitcast<float>(v[i] << 16) + sf_bitcast<float>(v[i] & 0xFFFF0000u);
     }
   }
 };
@@ -185,8 +227,8 @@ struct Act<SF_F32> {
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        hi[4 * q4 + j] = __builtin_bit_cast(bf16x2_t, (uint32_t)h[j] | ((uint32_t)h[j + 4] << 16));
-        lo[4 * q4 + j] = __builtin_bit_cast(bf16x2_t, (uint32_t)l[j] | ((uint32_t)l[j + 4] << 16));
+        hi[4 * q4 + j] = sf_bitcast<bf16x2_t>((uint32_t)h[j] | ((uint32_t)h[j + 4] << 16));
+        lo[4 * q4 + j] = sf_bitcast<bf16x2_t>((uint32_t)l[j] | ((uint32_t)l[j + 4] << 16));
       }
     }
   }
@@ -197,17 +239,17 @@ struct Act<SF_F32> {
 template <int XDT>
 __device__ __forceinline__ float chunk_dot(const u32x4 &wq, uint32_t z, const Act<XDT> &a) {
   if constexpr (XDT == SF_F16) {
-    const half2_t c1 = __builtin_bit_cast(half2_t, (0xE400u | z) * 0x10001u);        // -(1024+z)
-    const half2_t c2 = __builtin_bit_cast(half2_t, (0xD400u + 16u * z) * 0x10001u);  // -(64+z)
+    const half2_t c1 = sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);        // -(1024+z)
+    const half2_t c2 = sf_bitcast<half2_t>((0xD400u + 16u * z) * 0x10001u);  // -(64+z)
     const half2_t sixteenth = {(f16)0.0625f, (f16)0.0625f};
     float t = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t d = wq[j], d8 = d >> 8;
-      const half2_t v0 = __builtin_bit_cast(half2_t, (d & 0x000F000Fu) | 0x64006400u) + c1;
-      const half2_t v1 = __builtin_bit_cast(half2_t, (d & 0x00F000F0u) | 0x64006400u) * sixteenth + c2;
-      const half2_t v2 = __builtin_bit_cast(half2_t, (d8 & 0x000F000Fu) | 0x64006400u) + c1;
-      const half2_t v3 = __builtin_bit_cast(half2_t, (d8 & 0x00F000F0u) | 0x64006400u) * sixteenth + c2;
+      const half2_t v0 = sf_bitcast<half2_t>(and_or(d, 0x000F000Fu, 0x64006400u)) + c1;
+      const half2_t v1 = sf_bitcast<half2_t>(and_or(d, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
+      const half2_t v2 = sf_bitcast<half2_t>(and_or(d8, 0x000F000Fu, 0x64006400u)) + c1;
+      const half2_t v3 = sf_bitcast<half2_t>(and_or(d8, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
       t = __builtin_amdgcn_fdot2(v0, a.p[4 * j + 0], t, false);
       t = __builtin_amdgcn_fdot2(v1, a.p[4 * j + 1], t, false);
       t = __builtin_amdgcn_fdot2(v2, a.p[4 * j + 2], t, false);
@@ -221,7 +263,7 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &wq, uint32_t z, const Ac
       const uint32_t d = wq[j];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bf16x2_t v = __builtin_bit_cast(bf16x2_t, ((d >> (4 * i)) & 0x000F000Fu) | 0x43004300u);
+        const bf16x2_t v = sf_bitcast<bf16x2_t>(and_or(d >> (4 * i), 0x000F000Fu, 0x43004300u));
         if constexpr (XDT == SF_BF16) {
           t = __builtin_amdgcn_fdot2_f32_bf16(v, a.p[4 * j + i], t, false);
         } else {
@@ -254,38 +296,40 @@ k_q4_gemv(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
     for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
 
   if (c < C && row0 < N) {
-    // weights first: every load of the lane in flight before any math
-    u32x4 wv[R];
-    const uint8_t *wp = w + (size_t)row0 * Kh + (size_t)c * 16;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (row0 + r < N) wv[r] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)r * Kh));
-      else wv[r] = u32x4{0u, 0u, 0u, 0u};
-    }
+    // small, cache-resident operands first, then the weight stream, so each
+    // row's math can start as soon as its own 16 bytes arrive
     const int grp = c >> cpg_shift;
     const size_t cell = (size_t)(row0 >> 3) * G + grp;
     float sc[R];
-    ScaleLoad<R>::load(stile + cell * 8, row0, N, sc);
-    uint32_t zn = 0x88888888u;  // offset-binary symmetric codes: z = 8
-    if constexpr (ASYM) zn = load_zeros<R>(ztile + cell * 4, row0, N);
-
+    load_scales<R>(stile + cell * 8, (size_t)G * 8, row0, N, sc);
+    uint64_t zn = 0x8888888888888888ull;  // offset-binary symmetric codes: z = 8
+    if constexpr (ASYM) zn = load_zeros<R>(ztile + cell * 4, (size_t)G * 4, row0, N);
     Act<XDT> xa[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) xa[b].load(x, (size_t)b * K + (size_t)c * 32);
 
+    // Rows past N re-read row N-1 (no branch splits the load batch); their
+    // scales are the zero padding of the tiled scale array.
+    u32x4 wv[R];
+    const uint8_t *wp = w + (size_t)c * 16;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t z = (zn >> (4 * r)) & 15u;
+      const int row = min(row0 + r, N - 1);
+      wv[r] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)row * Kh));
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t z = (uint32_t)(zn >> (4 * r)) & 15u;
 #pragma unroll
       for (int b = 0; b < B; ++b) acc[b][r] = chunk_dot<XDT>(wv[r], z, xa[b]) * sc[r];
     }
   }
 
   const int p = tid & (Q - 1);
-  rowset_reduce<B, R, Q>(acc, p);
+  butterfly<B, R, Q / 2, R>(acc, p);
 
-  constexpr int LQ = Q == 64 ? 6 : 5;
-  constexpr int LR = R == 8 ? 3 : 2;
+  constexpr int LQ = clog2<Q>();
+  constexpr int LR = clog2<R>();
   constexpr int S = LR < LQ ? LR : LQ;
   constexpr int RF = R >> S;
   const int idx = p >> (LQ - S);
@@ -335,14 +379,26 @@ inline int ilog2(int v) {
   return l;
 }
 
-inline int plan_gemv(int B, int N, int K, int g, GemvPlan *pl) {
+// Rows per rowset. Defaults: 8 for batch <= 2, else 4 (register budget);
+// SF_GEMV_R in the environment overrides it within the instantiated set.
+inline int pick_rows(int B, int xdt) {
+  int r = B <= 2 ? 8 : 4;
+  if (const char *e = getenv("SF_GEMV_R")) {
+    const int v = atoi(e);
+    const bool ok = B <= 2 ? (v == 4 || v == 8 || (v == 16 && xdt != SF_F32)) : (v == 2 || v == 4);
+    if (ok) r = v;
+  }
+  return r;
+}
+
+inline int plan_gemv(int B, int N, int K, int g, int xdt, GemvPlan *pl) {
   pl->C = K / 32;
   pl->P = pl->C <= 32 ? 32 : ((pl->C + 63) / 64) * 64;
   SF_REQUIRE(pl->P <= 512, SF_EUNSUPPORTED, "in_features=%d exceeds this GEMV's limit of 16384", K);
   pl->Q = pl->P == 32 ? 32 : 64;
   pl->WG = pl->P <= 256 ? 256 : pl->P;
   pl->RS = pl->WG / pl->P;
-  pl->R = B <= 2 ? 8 : 4;
+  pl->R = pick_rows(B, xdt);
   const int rows_per_wg = pl->RS * pl->R;
   pl->grid = (N + rows_per_wg - 1) / rows_per_wg;
   pl->cpg_shift = ilog2(g / 32);
@@ -375,28 +431,38 @@ struct GemvArgs {
   const void *bias; int bdt; int B, N, K, G; bool asym; hipStream_t s;
 };
 
+template <int B, int X>
+void launch_b(const GemvPlan &pl, const GemvArgs &a) {
+#define SF_GEMV_R(RR) \
+  launch_bqx<B, RR, X>(pl, a.asym, a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.N, a.K, a.G, a.s)
+  if constexpr (B <= 2) {
+    if (pl.R == 4) SF_GEMV_R(4);
+    else if (pl.R == 16 && X != SF_F32) { if constexpr (X != SF_F32) SF_GEMV_R(16); }
+    else SF_GEMV_R(8);
+  } else {
+    if (pl.R == 2) SF_GEMV_R(2);
+    else SF_GEMV_R(4);
+  }
+#undef SF_GEMV_R
+}
+
 template <int X>
 void launch_x(const GemvPlan &pl, const GemvArgs &a) {
-#define SF_GEMV_CASE(BB, RR) \
-  case BB: launch_bqx<BB, RR, X>(pl, a.asym, a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.N, a.K, a.G, a.s); break;
   if constexpr (X == SF_F32) {  // fp32 activations: at most 2 rows per launch (registers)
+    if (a.B == 1) launch_b<1, X>(pl, a);
+    else launch_b<2, X>(pl, a);
+  } else {
     switch (a.B) {
-      SF_GEMV_CASE(1, 8)
-      SF_GEMV_CASE(2, 8)
+      case 1: launch_b<1, X>(pl, a); break;
+      case 2: launch_b<2, X>(pl, a); break;
+      case 3: launch_b<3, X>(pl, a); break;
+      case 4: launch_b<4, X>(pl, a); break;
+      case 5: launch_b<5, X>(pl, a); break;
+      case 6: launch_b<6, X>(pl, a); break;
+      case 7: launch_b<7, X>(pl, a); break;
+      default: launch_b<8, X>(pl, a); break;
     }
-    return;
   }
-  switch (a.B) {
-    SF_GEMV_CASE(1, 8)
-    SF_GEMV_CASE(2, 8)
-    SF_GEMV_CASE(3, 4)
-    SF_GEMV_CASE(4, 4)
-    SF_GEMV_CASE(5, 4)
-    SF_GEMV_CASE(6, 4)
-    SF_GEMV_CASE(7, 4)
-    SF_GEMV_CASE(8, 4)
-  }
-#undef SF_GEMV_CASE
 }
 
 }  // namespace sf_gemv

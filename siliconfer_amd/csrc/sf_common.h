@@ -69,13 +69,23 @@ static inline bool sf_blob_layout(int N, int K, int g, int has_zeros, BlobLayout
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
+// Bit reinterpretation by value. Applied directly to an ext_vector element
+// (`v.z`, `v[i]`), this compiler's __builtin_bit_cast reads element 0 instead;
+// taking the argument by value first makes every use safe, so kernel code
+// only uses sf_bitcast.
+template <class To, class From>
+__host__ __device__ __forceinline__ To sf_bitcast(From v) {
+  static_assert(sizeof(To) == sizeof(From), "sf_bitcast size mismatch");
+  return __builtin_bit_cast(To, v);
+}
+
 __device__ __forceinline__ float sf_bf16_to_f32(uint16_t b) {
-  return __builtin_bit_cast(float, (uint32_t)b << 16);
+  return sf_bitcast<float>((uint32_t)b << 16);
 }
 
 // round-to-nearest-even float -> bf16 bits (NaN kept quiet)
 __device__ __forceinline__ uint16_t sf_f32_to_bf16(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  uint32_t u = sf_bitcast<uint32_t>(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);

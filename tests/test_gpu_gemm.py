@@ -100,3 +100,19 @@ def test_gemm_bias_and_split_k_determinism(dev):
     first = w.matmul(xt, out_dtype=torch.float32).clone()
     for _ in range(5):
         assert torch.equal(w.matmul(xt, out_dtype=torch.float32), first)
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_gemm_unit_vector_rows_pin_mapping(dev, xdtype):
+    """Row m of X = e_{k(m)}: Y[m, n] = q[n, k(m)] * s[n, k(m)/g] exactly (one product)."""
+    rng = np.random.default_rng(31)
+    N, K, g, M = 136, 320, 64, 150
+    q = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    s = (np.arange(N * (K // g)).reshape(N, K // g) % 53 + 1).astype(np.float32) / 16
+    w = Q4Weight(P.pack_rows(q), s, None, g, device=dev)
+    kk = rng.integers(0, K, M)
+    X = np.zeros((M, K), np.float32)
+    X[np.arange(M), kk] = 1.0
+    Y = w.matmul(torch.as_tensor(X).to(dev).to(xdtype), out_dtype=torch.float32).cpu().numpy()
+    exp = (q[:, kk].astype(np.float64) * s[:, kk // g]).T
+    np.testing.assert_array_equal(Y, exp.astype(np.float32))

@@ -200,3 +200,24 @@ def test_repack_round_trip_bit_exact(dev, asym):
     np.testing.assert_array_equal(s2.cpu().numpy(), s.astype(np.float16))
     if asym:
         np.testing.assert_array_equal(z2.cpu().numpy(), z.astype(np.uint8))
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N,K,g", [(24, 64, 32), (40, 256, 64), (16, 2048, 128)])
+def test_unit_vector_activations_pin_row_and_k_mapping(dev, xdtype, N, K, g):
+    """x = e_k picks column k: y[n] = (q[n,k] - z) * s[n, k/g] exactly (one product),
+    with a distinct scale per (row, group). Any mix-up of rows, k positions,
+    batch rows or scale cells shows up as an exact mismatch."""
+    rng = np.random.default_rng(K)
+    q = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    pk = P.pack_rows(q)
+    s = (np.arange(N * (K // g)).reshape(N, K // g) % 61 + 1).astype(np.float32) / 8
+    w = Q4Weight(pk, s, None, g, device=dev)
+    ks = sorted(set([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 15, 16, 31, K - 1] + list(rng.integers(0, K, 10))))
+    for b0 in range(0, len(ks), 8):
+        kk = ks[b0:b0 + 8]
+        X = np.zeros((len(kk), K), np.float32)
+        X[np.arange(len(kk)), kk] = 1.0
+        y = w.matmul(torch.as_tensor(X).to(dev).to(xdtype), out_dtype=torch.float32).cpu().numpy()
+        exp = (q[:, kk].astype(np.float64) * s[:, np.array(kk) // g]).T
+        np.testing.assert_array_equal(y, exp.astype(np.float32))
