@@ -4,16 +4,24 @@ One step = one pass over config 3's sweep on one GPU: symmetric int4 RTN, group
 128, W in {[4096,4096], [11008,4096], [4096,11008]} x batch {1, 2, 4, 8}, fp16
 activations, fp32 accumulation — 12 GEMV launches. Every launch reads a
 different copy of its weight blob (>= 512 MB of copies per shape, twice the
-256 MB last-level cache), so the weights come from HBM. The step's launches are
-replayed from HIP graphs.
+256 MB last-level cache), so the weights come from HBM. The steps are replayed
+from HIP graphs.
 
 Printed JSON (one line):
   value         whole-job algorithmic GB/s: sum of per-launch algorithmic bytes
-                over the timed steps / wall time between HIP events bracketing
-                the K timed steps (inputs resident in HBM);
+                over the K timed steps / time between HIP events bracketing
+                them (inputs resident in HBM);
   roofline      the GEMV kernel: achieved = algorithmic bytes per launch /
-                average launch duration (HIP events around each launch on the
-                launch stream), against the 8 TB/s MI355X HBM peak;
+                average launch duration. The average comes from HIP events
+                around a graph of back-to-back launches of the same case on
+                the launch stream (an event pair around one launch has a ~6 us
+                floor of its own); `traffic` is the HBM bytes per launch that
+                rocprofv3 FETCH_SIZE + WRITE_SIZE counters measured
+                (profiles/gemv_sweep_pmc.json, calibrated on a copy of known
+                size), when that file is present;
+  secondary     the other hot-path kernels at their BASELINE configs, timed the
+                same way: config-1 GEMV, config-2 prefill GEMM, config-4
+                decode attention, the KV-cache append;
   cpu_baseline  the reference's own CPU kernel (q4_gemv.cpp / q4_gemm.cpp,
                 compiled from /root/reference into oracle/_ref) or, when that
                 library is absent, the C restatement oracle/q4_cpu.c, on a
@@ -24,6 +32,7 @@ Algorithmic bytes per launch (B = batch): N*K/2 (int4) + 2*N*K/128 (fp16
 scales) + 2*B*K (fp16 x) + 2*B*N (fp16 y).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --profile-kernels   (eager launches for rocprofv3 runs)
 """
 
 from __future__ import annotations
@@ -37,23 +46,65 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]
 BATCHES = [1, 2, 4, 8]
 GROUP = 128
 COLD_BYTES = 512 << 20
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PMC_FILE = os.path.join(ROOT, "profiles", "gemv_sweep_pmc.json")
 
 
-def alg_bytes(N: int, K: int, B: int, g: int = GROUP) -> int:
-    return N * K // 2 + 2 * N * (K // g) + 2 * B * K + 2 * B * N
+def alg_bytes(N: int, K: int, B: int, g: int = GROUP, zeros: bool = False) -> int:
+    z = N * (K // g) // 2 if zeros else 0
+    return N * K // 2 + 2 * N * (K // g) + z + 2 * B * K + 2 * B * N
 
 
-def quantize_shape(N, K, seed):
-    """Config-3 synthetic weights: W ~ N(0, 0.02) RTN-quantized, symmetric, g=128."""
+def quantize_shape(N, K, seed, g=GROUP):
+    """Config-3 synthetic weights: W ~ N(0, 0.02) RTN-quantized, symmetric."""
     from siliconfer_amd.kernels import pack_weights_sym
 
     rng = np.random.default_rng(seed)
     W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
-    return pack_weights_sym(W, GROUP)
+    return pack_weights_sym(W, g)
+
+
+def cold_copies(t, nbytes):
+    """t plus clones so that the set spans >= COLD_BYTES."""
+    n = max(2, -(-COLD_BYTES // max(nbytes, 1)))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+class Timer:
+    """Average duration of a launch sequence: HIP events around graph replays.
+    With eager=True it only launches each call once (profiling runs)."""
+
+    def __init__(self, torch, stream, eager=False):
+        self.torch, self.stream, self.eager = torch, stream, eager
+
+    def per_call_us(self, fns, reps=4):
+        torch = self.torch
+        if self.eager:
+            with torch.cuda.stream(self.stream):
+                for f in fns:
+                    f()
+            torch.cuda.synchronize()
+            return float("nan")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            for f in fns:
+                f()
+        with torch.cuda.stream(self.stream):
+            g.replay()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(self.stream)
+            for _ in range(reps):
+                g.replay()
+            b.record(self.stream)
+            torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (reps * len(fns))
 
 
 class GpuSweep:
@@ -74,10 +125,9 @@ class GpuSweep:
         for i, (N, K) in enumerate(SHAPES):
             pk, s = quantize_shape(N, K, 2 + i)
             w = Q4Weight(pk, s, None, GROUP, device=dev)
-            copies = max(2, -(-COLD_BYTES // w.nbytes))
-            blobs = [w.blob] + [w.blob.clone() for _ in range(copies - 1)]
+            blobs = cold_copies(w.blob, w.nbytes)
             self.keep += blobs
-            self.n_rot = max(self.n_rot, copies)
+            self.n_rot = max(self.n_rot, len(blobs))
             x = torch.as_tensor(rng.normal(0, 1, (8, K)).astype(np.float16)).to(dev)
             self.keep.append(x)
             for B in BATCHES:
@@ -90,7 +140,7 @@ class GpuSweep:
     def launch(self, ci: int, rot: int) -> None:
         N, K, B, blobs, xp, yp = self.cases[ci]
         rc = self.lib.sf_q4_gemv(blobs[rot % len(blobs)], xp, 1, yp, 1, None, None, 0, B, N, K,
-                                 GROUP, 0, self.stream.cuda_stream)
+                                 GROUP, 0, self.torch.cuda.current_stream().cuda_stream)
         if rc != 0:
             raise RuntimeError(self.lib.sf_last_error().decode())
 
@@ -106,7 +156,7 @@ class GpuSweep:
             with torch.cuda.graph(g, stream=self.stream):
                 self.eager_step(rot)
             self.graphs.append(g)
-        self.torch.cuda.synchronize()
+        torch.cuda.synchronize()
 
     def step(self, i: int) -> None:
         if self.graphs is not None:
@@ -114,22 +164,99 @@ class GpuSweep:
         else:
             self.eager_step(i)
 
-    def per_launch_us(self, reps: int):
-        """Average duration of each case's launch, from HIP event pairs around it."""
-        torch = self.torch
+    def per_case_us(self):
+        timer = Timer(self.torch, self.stream)
         out = []
-        with torch.cuda.stream(self.stream):
-            for ci in range(len(self.cases)):
-                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                      for _ in range(reps)]
-                for r in range(reps):
-                    ev[r][0].record(self.stream)
-                    self.launch(ci, r + 1)
-                    ev[r][1].record(self.stream)
-                self.stream.synchronize()
-                ts = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-                out.append(float(np.mean(ts)))
+        for ci, (N, K, B, blobs, *_) in enumerate(self.cases):
+            fns = [(lambda r=r, ci=ci: self.launch(ci, r)) for r in range(len(blobs))]
+            out.append(timer.per_call_us(fns))
         return out
+
+
+def secondary(dev, stream, eager=False):
+    """The other hot-path kernels at their BASELINE configs (cold HBM, graph-timed)."""
+    import torch
+
+    from siliconfer_amd import _lib
+    from siliconfer_amd.kernels import Q4Weight, pack_weights_asym
+
+    lib = _lib.load()
+    timer = Timer(torch, stream, eager)
+    cur = lambda: torch.cuda.current_stream().cuda_stream
+    out = {}
+    rng = np.random.default_rng(0)
+
+    # config 1: [4864, 896] sym g=64, B=1
+    pk, s = quantize_shape(4864, 896, 0, g=64)
+    w = Q4Weight(pk, s, None, 64, device=dev)
+    blobs = cold_copies(w.blob, w.nbytes)
+    x = torch.as_tensor(rng.normal(0, 1, (1, 896)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 4864), dtype=torch.float16, device=dev)
+    us = timer.per_call_us([(lambda b=b: lib.sf_q4_gemv(b.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 1,
+                                                        None, None, 0, 1, 4864, 896, 64, 0, cur()))
+                            for b in blobs])
+    nb = alg_bytes(4864, 896, 1, 64)
+    out["config1_gemv_4864x896_g64_b1"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
+                                           "bytes": nb}
+    del blobs, w
+
+    # config 2: asym prefill GEMM, X bf16 [512, K], up/gate [4864, 896] and down [896, 4864]
+    for (N, K) in [(4864, 896), (896, 4864)]:
+        W = rng.laplace(0, 0.015, (N, K)).astype(np.float32)
+        pa, sa, za = pack_weights_asym(W, 64)
+        wq = Q4Weight(pa, sa, za, 64, device=dev)
+        X = torch.as_tensor(rng.normal(0, 1, (512, K)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        Y = torch.empty((512, N), dtype=torch.bfloat16, device=dev)
+        wsb = lib.sf_q4_gemm_workspace_bytes(512, N, K, 64)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        blobs = cold_copies(wq.blob, wq.nbytes)
+        fns = [(lambda b=b: lib.sf_q4_gemm(b.data_ptr(), X.data_ptr(), 2, Y.data_ptr(), 2, None, None,
+                                           0, 512, N, K, 64, 1, ws.data_ptr() if wsb else None, wsb,
+                                           cur())) for b in blobs]
+        us = timer.per_call_us(fns, reps=2)
+        flops = 2.0 * 512 * N * K
+        out[f"config2_gemm_asym_m512_{N}x{K}"] = {
+            "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
+            "mfma_frac_of_bf16_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del blobs, wq
+
+    # config 4: decode attention over an int8 cache, fp16 scales, q fp16 [1, 14, 64]
+    for T in (4096, 16384):
+        kc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
+        vc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
+        ks = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+        vs = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+        q = torch.randn((1, 14, 64), device=dev).half()
+        o = torch.empty((1, 14, 64), dtype=torch.float16, device=dev)
+        per = kc.numel() * 2 + ks.numel() * 4
+        n = max(2, -(-COLD_BYTES // per))
+        sets = [(kc, ks, vc, vs)] + [(kc.clone(), ks.clone(), vc.clone(), vs.clone())
+                                     for _ in range(n - 1)]
+        nsp = lib.sf_attn_default_splits(1, 2, T)
+        ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
+        wsp = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
+                                                    a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
+                                                    1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
+                                                    0.125, nsp, cur())) for a in sets]
+        us = timer.per_call_us(fns)
+        nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
+        out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
+                                     "bytes": nb, "splits": nsp,
+                                     "launches": "split kernel + combine kernel"}
+        del sets
+
+    # KV append: one decode token, [1, 2, 1, 64] fp16 K and V into a 4096-slot cache
+    qk = torch.empty((1, 2, 4096, 64), dtype=torch.int8, device=dev)
+    sk = torch.empty((1, 2, 4096), dtype=torch.float16, device=dev)
+    qv, sv = torch.empty_like(qk), torch.empty_like(sk)
+    kn = torch.randn((1, 2, 1, 64), device=dev).half()
+    vn = torch.randn((1, 2, 1, 64), device=dev).half()
+    fns = [(lambda t=t: lib.sf_kv_quant_append(kn.data_ptr(), vn.data_ptr(), 1, qk.data_ptr(),
+                                               sk.data_ptr(), qv.data_ptr(), sv.data_ptr(), 1, 1, 2,
+                                               1, t, 4096, 64, cur())) for t in range(64)]
+    out["kv_append_1tok_2heads_d64"] = {"us": round(timer.per_call_us(fns), 3)}
+    return out
 
 
 def cpu_baseline(budget_s: float):
@@ -192,16 +319,108 @@ def cpu_baseline(budget_s: float):
     }
 
 
+def profile_kernels(dev) -> None:
+    """Eager launches for rocprofv3 (trace or counters): each sweep case over its
+    cold copies, a 256 MiB device copy (read 256 MiB + write 256 MiB) that
+    calibrates FETCH_SIZE / WRITE_SIZE, then the secondary kernels' cases."""
+    import torch
+
+    sweep = GpuSweep(dev)
+    with torch.cuda.stream(sweep.stream):
+        for ci, (N, K, B, blobs, *_) in enumerate(sweep.cases):
+            for r in range(len(blobs)):
+                sweep.launch(ci, r)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    secondary(dev, sweep.stream, eager=True)
+    print(json.dumps({"profile_kernels": [f"{N}x{K} B={B} x{len(b)}" for N, K, B, b, *_ in sweep.cases],
+                      "calibration_copy_bytes": 256 << 20}))
+
+
+def _short_kernel(name: str) -> str:
+    import re
+
+    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)", name)
+    if m:
+        return f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},x={m.group(5)}>"
+    m = re.search(r"(k_[a-z0-9_]+|__amd_rocclr_[A-Za-z]+|at::native::[a-z_]+)", name)
+    return m.group(1) if m else name[:40]
+
+
+def summarize_profile(trace_csv=None, fetch_csv=None, write_csv=None) -> dict:
+    """Summaries of rocprofv3 CSV outputs of `bench.py --profile-kernels`:
+    per (kernel, grid) duration stats from a --kernel-trace run, and per
+    (kernel, grid) HBM bytes from FETCH_SIZE / WRITE_SIZE runs, scaled by what
+    the counters read for the 256 MiB calibration copy (the largest copy)."""
+    import csv
+    import statistics
+
+    out = {}
+    if trace_csv:
+        agg = {}
+        for r in csv.DictReader(open(trace_csv)):
+            key = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]),
+                   int(r["Workgroup_Size_X"]))
+            agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out["durations_us"] = [
+            {"kernel": k[0], "grid_threads": k[1], "wg": k[2], "n": len(v),
+             "mean": round(statistics.fmean(v), 3), "median": round(statistics.median(v), 3),
+             "min": round(min(v), 3)} for k, v in agg.items() if len(v) >= 2]
+    if fetch_csv and write_csv:
+        def load(p):
+            agg = {}
+            for r in csv.DictReader(open(p)):
+                key = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size"]))
+                agg.setdefault(key, []).append(float(r["Counter_Value"]))
+            return agg
+        f, w = load(fetch_csv), load(write_csv)
+        # the calibration copy is the largest copy dispatch in the run
+        copy_kib = (256 << 20) / 1024
+        ff = copy_kib / max(v for k, vs in f.items() if "copyBuffer" in k[0] for v in vs)
+        wf = copy_kib / max(v for k, vs in w.items() if "copyBuffer" in k[0] for v in vs)
+        rows = []
+        for k in f:
+            if k not in w or "copyBuffer" in k[0]:
+                continue
+            rows.append({"kernel": k[0], "grid_threads": k[1], "n": len(f[k]),
+                         "fetch_bytes": int(statistics.median(f[k]) * ff * 1024),
+                         "write_bytes": int(statistics.median(w[k]) * wf * 1024)})
+        out["hbm_traffic"] = {"fetch_scale": round(ff, 4), "write_scale": round(wf, 4),
+                              "calibration": "256 MiB device copy", "per_launch": rows}
+    return out
+
+
+def load_traffic():
+    try:
+        with open(PMC_FILE) as f:
+            d = json.load(f)
+        return d.get("hbm_bytes_per_launch_avg"), d
+    except (OSError, ValueError):
+        return None, None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the other kernels' timings")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of reference CPU work")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
-    ap.add_argument("--event-reps", type=int, default=50)
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only run eager launches of every case (for rocprofv3)")
+    ap.add_argument("--summarize-profile", nargs="+", metavar="CSV",
+                    help="TRACE_CSV [FETCH_CSV WRITE_CSV]: summarize rocprofv3 output and exit")
     args = ap.parse_args()
+
+    if args.summarize_profile:
+        paths = args.summarize_profile + [None] * 3
+        print(json.dumps(summarize_profile(*paths[:3]), indent=1))
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; --gpus must be 1 "
@@ -216,6 +435,10 @@ def main() -> int:
         raise SystemExit("bench.py needs a gfx950 GPU and the built libsiliconfer_hip.so")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.profile_kernels:
+        profile_kernels(dev)
+        return 0
+
     sweep = GpuSweep(dev)
     if not args.eager:
         sweep.capture()
@@ -235,13 +458,14 @@ def main() -> int:
     ms_per_step = total_ms / args.steps
     value = sweep.step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    us = sweep.per_launch_us(args.event_reps)
+    us = sweep.per_case_us()
     case_bytes = [alg_bytes(N, K, B) for N, K, B, *_ in sweep.cases]
     achieved = sum(case_bytes) / (sum(us) * 1e-6) / 1e9
     cases = [{"N": N, "K": K, "B": B, "us": round(t, 3),
               "GBps": round(b / (t * 1e-6) / 1e9, 1)}
              for (N, K, B, *_), t, b in zip(sweep.cases, us, case_bytes)]
-
+    traffic, _ = load_traffic()
+    sec = None if args.no_secondary else secondary(dev, sweep.stream)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
 
     line = {
@@ -269,10 +493,13 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "sf_q4_gemv (k_q4_gemv), per-launch HIP events, cold HBM",
+            "traffic": traffic,
+            "kernel": "k_q4_gemv via sf_q4_gemv; average over the 12 sweep cases, each timed "
+                      "as a graph of back-to-back cold launches between HIP events",
+            "alg_bytes_per_launch_avg": int(sum(case_bytes) / len(case_bytes)),
         },
         "cases": cases,
+        "secondary": sec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -260,26 +260,65 @@ k_attn_split(const void *__restrict__ q, const int8_t *__restrict__ kc,
   }
 }
 
-__global__ void __launch_bounds__(256)
+// Merge the split partials of one (b, h): M = max m_s, c_s = 2^(m_s - M),
+// out = sum_s c_s acc_s / max(sum_s c_s l_s, 1e-20) (q4_attention.py:256-261).
+// The block first reduces M and L over the splits in parallel, keeps c_s in
+// LDS, then (dim, split-slice) threads sum their slice and fold through LDS.
+constexpr int kCombineThreads = 256;
+constexpr int kMaxSplits = 2048;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float *scratch) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = sf_shfl_xor(v, off);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  v = scratch[0];
+  for (int w = 1; w < kCombineThreads / 64; ++w) v = is_max ? fmaxf(v, scratch[w]) : v + scratch[w];
+  return v;
+}
+
+__global__ void __launch_bounds__(kCombineThreads)
 k_attn_combine(const float *__restrict__ part_acc, const float *__restrict__ part_ml,
                void *__restrict__ out, int odt, int D, int n_splits) {
+  __shared__ float c_s[kMaxSplits];
+  __shared__ float scratch[kCombineThreads / 64];
+  __shared__ float fold[kCombineThreads];
   const size_t bh = blockIdx.x;
+  const int tid = threadIdx.x;
   const float *ml = part_ml + bh * n_splits * 2;
-  float M = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ml[2 * s]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float L = 0.f, A = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < n_splits; ++s) {
-        const float c = __builtin_amdgcn_exp2f(ml[2 * s] - M);
-        L = fmaf(ml[2 * s + 1], c, L);
-        A = fmaf(part_acc[(bh * n_splits + s) * D + d], c, A);
-      }
-    }
-    const float v = A / fmaxf(L, 1e-20f);
-    if (odt == SF_F32) ((float *)out)[bh * D + d] = v;
-    else if (odt == SF_F16) ((f16 *)out)[bh * D + d] = (f16)v;
-    else ((uint16_t *)out)[bh * D + d] = sf_f32_to_bf16(v);
+  float mx = -INFINITY;
+  for (int s = tid; s < n_splits; s += kCombineThreads) mx = fmaxf(mx, ml[2 * s]);
+  const float M = block_reduce(mx, true, scratch);
+  float lsum = 0.f;
+  for (int s = tid; s < n_splits; s += kCombineThreads) {
+    const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[2 * s] - M);
+    c_s[s] = c;
+    lsum = fmaf(ml[2 * s + 1], c, lsum);
+  }
+  const float L = block_reduce(lsum, false, scratch);  // also orders the c_s writes
+  const float inv = 1.f / fmaxf(L, 1e-20f);
+  // dims over lanes, splits over slices
+  const int nslice = kCombineThreads / D > 0 ? kCombineThreads / D : 1;
+  const int d = tid % D, slice = tid / D;
+  float a = 0.f;
+  if (slice < nslice && d < D) {
+    const float *pa = part_acc + bh * n_splits * D + d;
+#pragma unroll 4
+    for (int s = slice; s < n_splits; s += nslice) a = fmaf(pa[(size_t)s * D], c_s[s], a);
+  }
+  fold[tid] = a;
+  __syncthreads();
+  for (int dd = tid; dd < D; dd += kCombineThreads) {
+    float v = 0.f;
+    for (int sl = 0; sl < nslice; ++sl) v += fold[sl * D + dd];
+    v *= inv;
+    if (odt == SF_F32) ((float *)out)[bh * D + dd] = v;
+    else if (odt == SF_F16) ((f16 *)out)[bh * D + dd] = (f16)v;
+    else ((uint16_t *)out)[bh * D + dd] = sf_f32_to_bf16(v);
   }
 }
 
@@ -368,6 +407,7 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
   if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T);
   // the reference's tiling: n_tiles = max(1, min(n_tiles, T)); tile = ceil(T / n_tiles)
   n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
+  if (n_splits > kMaxSplits) n_splits = kMaxSplits;
   if (n_splits < 1) n_splits = 1;
   const int tile = T > 0 ? (T + n_splits - 1) / n_splits : 0;
   const size_t need = sf_attn_workspace_bytes(B, H, D, n_splits);
@@ -399,6 +439,6 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
 #undef SF_ATTN_LAUNCH
   int rc = sf_check_launch("sf_attn_decode_i8kv(split)");
   if (rc) return rc;
-  k_attn_combine<<<B * H, 64, 0, st>>>(part_acc, part_ml, out, out_dtype, D, n_splits);
+  k_attn_combine<<<B * H, kCombineThreads, 0, st>>>(part_acc, part_ml, out, out_dtype, D, n_splits);
   return sf_check_launch("sf_attn_decode_i8kv(combine)");
 }
