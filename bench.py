@@ -234,7 +234,7 @@ def secondary(dev, stream, eager=False):
                                      for _ in range(n - 1)]
         nsp = lib.sf_attn_default_splits(1, 2, T)
         ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
-        wsp = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        wsp = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
         fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
                                                     a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
                                                     1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
@@ -243,7 +243,7 @@ def secondary(dev, stream, eager=False):
         nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
         out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
                                      "bytes": nb, "splits": nsp,
-                                     "launches": "split kernel + combine kernel"}
+                                     "launches": "one (splits + fused merge)"}
         del sets
 
     # KV append: one decode token, [1, 2, 1, 64] fp16 K and V into a 4096-slot cache

@@ -112,9 +112,15 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
  * with K = k_codes * k_scales per token (likewise V). Replaces
  * fused_quantized_attention_decode (siliconfer/kernels/metal/q4_attention.py:
  * 200-261). q: [B, H, D] of q_dtype; out: [B, H, D] of out_dtype. n_splits is
- * the split-T count (the reference's n_tiles; <=0 picks a default). D <= 256
- * (the reference's bound, q4_attention.py:78,227-228) and D % 8 == 0.
- * workspace: sf_attn_workspace_bytes(B, H, D, n_splits) bytes. */
+ * the split-T count (the reference's n_tiles; <=0 picks a default; at most
+ * 512). D <= 256 (the reference's bound, q4_attention.py:78,227-228) and
+ * D % 8 == 0. One launch: the splits' partials are merged by the last split
+ * to finish.
+ * workspace: sf_attn_workspace_bytes(B, H, D, n_splits) bytes, 256-byte
+ * aligned, ZERO-FILLED before its first use. Its first 16 KiB hold merge
+ * counters that every call leaves at zero, so one workspace serves later
+ * calls of any shape. Calls that share a workspace must not overlap (use one
+ * workspace per stream). */
 size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
 int sf_attn_default_splits(int B, int KVH, int T);
 int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const void *k_scales,

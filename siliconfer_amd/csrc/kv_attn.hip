@@ -15,11 +15,14 @@
 //  * one workgroup per (split, kv head, head block, b) serves ALL the query
 //    heads that share the kv head (GQA) from one read of the K/V codes — the
 //    reference's kernel re-reads each kv head once per query head (:103);
-//  * inside a split, 64-token sub-tiles: scores with lanes along D (8 codes
-//    per lane, one 8-byte load), a per-head running max / sum in base 2
-//    (scores pre-scaled by log2 e), then P.V with lanes along D again;
-//  * the split partials (m, l, acc[D]) are merged by a second kernel with the
-//    reference's combine rule (q4_attention.py:63-70, 256-261).
+//  * inside a split, lanes are (token, 8-dim octet) with all query heads of
+//    the block in registers; each lane keeps its own online softmax (in base
+//    2, scores pre-scaled by log2 e) over its tokens, loading K and V codes
+//    with 8-byte loads a batch ahead; the lane states are merged through LDS;
+//  * the split partials (m, l, acc[D]) go to a workspace; the last workgroup
+//    of each (b, kv head, head block) to finish merges them in the same
+//    launch with the reference's combine rule (q4_attention.py:63-70,
+//    256-261); a single split writes the output directly.
 #include <math.h>
 
 #include "sf_common.h"
@@ -27,8 +30,6 @@
 namespace {
 
 constexpr int kAttnThreads = 256;
-constexpr int kSubTile = 64;
-constexpr int kHeadsPerBlock = 8;
 
 // ---------------------------------------------------------------------------
 // KV quantize + append
@@ -84,242 +85,434 @@ k_kv_quant_append(const void *__restrict__ k_new, const void *__restrict__ v_new
 }
 
 // ---------------------------------------------------------------------------
-// split-T decode attention
+// split-T decode attention, combine fused into the same launch
 // ---------------------------------------------------------------------------
-template <int QDT, int SDT>
+constexpr int kMaxD = 256;
+constexpr int kMaxSplits = 512;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr int kAttnBatch = 4;  // rows per lane per load batch
+constexpr int kMergeChunk = 32;  // partials per thread loaded at once by the merge
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// v + value of the lane at distance `off` in an aligned group of 2*off lanes
+// (DPP for off <= 8; the mirror patterns pair a lane with one of the other
+// half, and by symmetry every lane of the group ends with the full sum).
+__device__ __forceinline__ float add_partner(float v, int off) {
+  switch (off) {
+    case 1: return v + dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+    case 2: return v + dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    case 4: return v + dpp_f<0x141>(v);   // row_half_mirror
+    case 8: return v + dpp_f<0x140>(v);   // row_mirror
+    default: return v + __shfl_xor(v, off, 64);
+  }
+}
+
+__device__ __forceinline__ float max_partner(float v, int off) {
+  switch (off) {
+    case 1: return fmaxf(v, dpp_f<0xB1>(v));
+    case 2: return fmaxf(v, dpp_f<0x4E>(v));
+    case 4: return fmaxf(v, dpp_f<0x141>(v));
+    case 8: return fmaxf(v, dpp_f<0x140>(v));
+    default: return fmaxf(v, __shfl_xor(v, off, 64));
+  }
+}
+
+// max / sum over aligned groups of 32 lanes; every lane gets the result
+__device__ __forceinline__ float group32_max(float v) {
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) v = max_partner(v, off);
+  return v;
+}
+__device__ __forceinline__ float group32_sum(float v) {
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) v = add_partner(v, off);
+  return v;
+}
+
+__device__ __forceinline__ void i8x8_to_f32(u32x2 c, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = (float)(int8_t)(c.x >> (8 * i));
+    f[4 + i] = (float)(int8_t)(c.y >> (8 * i));
+  }
+}
+
+// Data handed between workgroups (split partials, merge counters) moves with
+// agent-scope relaxed atomics: they are coherent across the XCDs' L2 caches
+// by themselves, without the whole-L2 write-back / invalidate that an
+// agent-scope release / acquire fence costs. Order comes from completion:
+// the partial stores are waited for (vmcnt 0) before the counter increment,
+// and the merge's loads are issued only after the increment has returned.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store((uint32_t *)p, sf_bitcast<uint32_t>(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2_t ld2_agent(const float *p) {
+  return sf_bitcast<float2_t>(
+      __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int HB>
+constexpr int attn_smem_floats() {
+  // main phase: acc [NS][HB][D] (NS * D <= 2048 per head), m and l [NS][HB]
+  // (NS <= 256), M and L [HB]; merge phase: slice sums [NT] float4, split
+  // weights and l [HB][kMaxSplits] each, L [HB]
+  constexpr int a = 2048 * HB + 2 * 256 * HB + 2 * HB;
+  constexpr int b = 4 * kAttnThreads + 2 * HB * kMaxSplits + HB;
+  return a > b ? a : b;
+}
+
+// One workgroup per (split, kv head, block of HB query heads, batch row); the
+// split covers `tile` tokens. Lanes are (token, 8-dim octet): OCT lanes hold
+// one token's K and V codes (an 8-byte load each), so each code is converted
+// once for all HB heads of the block, whose q octets (pre-scaled by
+// scale * log2 e) sit in registers. A row is the 64 / OCT tokens one load
+// instruction covers; wave w walks rows w, w + 4, ... in batches of
+// kAttnBatch rows with the next batch's loads in flight, and each lane keeps
+// its own online-softmax state per head (m, l, acc[8]) with no block-level
+// synchronisation. At the end the NS = 4 * 64 / OCT lane states of each head
+// are merged through LDS into the split's partial; with one split it is the
+// output, otherwise the last workgroup of the (b, kv head, head block) group
+// to finish (device-scope counter) merges all splits' partials with the
+// reference's rule, writes the output and resets the counter.
+template <int QDT, int SDT, int HB>
 __global__ void __launch_bounds__(kAttnThreads)
-k_attn_split(const void *__restrict__ q, const int8_t *__restrict__ kc,
-             const void *__restrict__ ks, const int8_t *__restrict__ vc,
-             const void *__restrict__ vs, float *__restrict__ part_acc,
-             float *__restrict__ part_ml, int H, int KVH, int T, int T_cap, int D,
-             float qscale, int n_splits, int tile, int tpt_log2) {
-  constexpr int HB = kHeadsPerBlock;
-  extern __shared__ float red[];  // [4 waves][HB][D]
-  __shared__ float sc[HB][kSubTile];
-  __shared__ float m_s[HB], l_s[HB], c_s[HB];
+k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
+              const void *__restrict__ ks, const int8_t *__restrict__ vc,
+              const void *__restrict__ vs, float *part_acc, float *part_ml, unsigned *counters,
+              void *__restrict__ out, int odt, int H, int KVH, int T, int T_cap, int D,
+              float qscale, int n_splits, int tile, int oct_log2) {
+  constexpr int NT = kAttnThreads, NW = kAttnWaves, U = kAttnBatch;
+  __shared__ __attribute__((aligned(16))) float smem[attn_smem_floats<HB>()];
+  __shared__ int s_last;
+
+  const int OCT = 1 << oct_log2;  // lanes per token
+  const int R = 64 >> oct_log2;   // tokens per row
+  const int NS = NW * R;          // lane states per head in the workgroup
 
   const int split = blockIdx.x;
   const int G = H / KVH;
   const int n_hblk = (G + HB - 1) / HB;
   const int kvh = blockIdx.y / n_hblk;
-  const int h0 = (blockIdx.y - kvh * n_hblk) * HB;  // first query head (within the group)
-  const int nh = min(HB, G - h0);
+  const int hblk = blockIdx.y - kvh * n_hblk;
+  const int nh = min(HB, G - hblk * HB);
   const int b = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int tpt = 1 << tpt_log2;  // lanes per token (8 codes each)
-  const int ds = tid & (tpt - 1);
-  const int tsub = tid >> tpt_log2;
-  const int nsub = kAttnThreads >> tpt_log2;
-  const int d0 = ds * 8;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int oct = lane & (OCT - 1);
+  const int grp = lane >> oct_log2;
+  const int slot = wave * R + grp;
+  const int d0 = oct * 8;
   const bool dact = d0 < D;
+  const int dq = dact ? d0 : 0;
+  const int t0 = split * tile, t1 = min(t0 + tile, T);
+  const size_t base = ((size_t)b * KVH + kvh) * (size_t)T_cap;
+  const size_t bh0 = (size_t)b * H + (size_t)kvh * G + (size_t)hblk * HB;
 
-  const int t0 = split * tile;
-  const int t1 = min(t0 + tile, T);
-
-  // query slice for this lane's 8 dims, pre-scaled by softmax scale * log2(e)
   float qr[HB][8];
 #pragma unroll
-  for (int h = 0; h < HB; ++h)
+  for (int h = 0; h < HB; ++h) {
+    sf_load8_as_f32<QDT>(q, (bh0 + min(h, nh - 1)) * D + dq, qr[h]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = 0.f;
-      if (h < nh && dact && d0 + i < D)
-        v = sf_load_as_f32<QDT>(q, ((size_t)b * H + (size_t)kvh * G + h0 + h) * D + d0 + i) * qscale;
-      qr[h][i] = v;
-    }
-  float acc[HB][8];
+    for (int i = 0; i < 8; ++i) qr[h][i] = (h < nh && dact) ? qr[h][i] * qscale : 0.f;
+  }
+
+  float m[HB], l[HB], acc[HB][8];
 #pragma unroll
-  for (int h = 0; h < HB; ++h)
+  for (int h = 0; h < HB; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-  if (tid < HB) {
-    m_s[tid] = -INFINITY;
-    l_s[tid] = 0.f;
   }
-  __syncthreads();
 
-  const size_t base = ((size_t)b * KVH + kvh) * (size_t)T_cap;
-  const int wave = tid >> 6, lane = tid & 63;
-
-  for (int tt = t0; tt < t1; tt += kSubTile) {
-    const int n = min(kSubTile, t1 - tt);
-    // ---- scores
-    for (int j = tsub; j < kSubTile; j += nsub) {
-      float part[HB];
+  struct Batch {
+    u32x2 k[U], v[U];
+    float ks[U], vs[U];
+  };
+  // row step k of this wave covers tokens t0 + (wave + NW k) R + [0, R)
+  const int nrows = (t1 - t0 + R - 1) / R;
+  const int nsteps = (nrows + NW - 1) / NW;
+  auto token = [&](int k) { return t0 + (wave + NW * k) * R + grp; };
+  auto load = [&](int k0, Batch &bt) {
 #pragma unroll
-      for (int h = 0; h < HB; ++h) part[h] = 0.f;
-      if (j < n && dact) {
-        const int8_t *kp = kc + (base + tt + j) * (size_t)D + d0;
-        float kf[8];
-        if (d0 + 8 <= D) {
-          const uint64_t kv = *(const uint64_t *)kp;
+    for (int u = 0; u < U; ++u) {
+      const int t = min(token(k0 + u), t1 - 1);  // past the end: re-read, masked
+      const size_t row = base + t;
+      bt.k[u] = *(const u32x2 *)(kc + row * D + dq);
+      bt.v[u] = *(const u32x2 *)(vc + row * D + dq);
+      bt.ks[u] = sf_load_as_f32<SDT>(ks, row);
+      bt.vs[u] = sf_load_as_f32<SDT>(vs, row);
+    }
+  };
+  auto compute = [&](int k0, const Batch &bt) {
+    float s[U][HB];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) kf[i] = (float)(int8_t)(kv >> (8 * i));
-        } else {
+    for (int u = 0; u < U; ++u) {
+      float kf[8];
+      i8x8_to_f32(bt.k[u], kf);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) kf[i] = d0 + i < D ? (float)kp[i] : 0.f;
-        }
+      for (int h = 0; h < HB; ++h) {
+        float a = 0.f;
 #pragma unroll
-        for (int h = 0; h < HB; ++h)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) part[h] = fmaf(qr[h][i], kf[i], part[h]);
-      }
-      for (int off = tpt >> 1; off >= 1; off >>= 1)
-#pragma unroll
-        for (int h = 0; h < HB; ++h) part[h] += sf_shfl_xor(part[h], off);
-      if (ds == 0 && j < n) {
-        const float ksc = sf_load_as_f32<SDT>(ks, base + tt + j);
-#pragma unroll
-        for (int h = 0; h < HB; ++h)
-          if (h < nh) sc[h][j] = part[h] * ksc;
+        for (int i = 0; i < 8; ++i) a = fmaf(qr[h][i], kf[i], a);
+        s[u][h] = a;
       }
     }
-    __syncthreads();
-    // ---- running softmax statistics, one wave per head
-    for (int h = wave; h < nh; h += kAttnThreads / 64) {
-      float mx = -INFINITY;
-      for (int j = lane; j < n; j += 64) mx = fmaxf(mx, sc[h][j]);
-      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, sf_shfl_xor(mx, off));
-      const float m_old = m_s[h];
-      const float m_new = fmaxf(m_old, mx);
-      float sum = 0.f;
-      for (int j = lane; j < n; j += 64) {
-        const float p = __builtin_amdgcn_exp2f(sc[h][j] - m_new);
-        sc[h][j] = p;
-        sum += p;
-      }
-      for (int off = 32; off >= 1; off >>= 1) sum += sf_shfl_xor(sum, off);
-      if (lane == 0) {
-        const float c = __builtin_amdgcn_exp2f(m_old - m_new);  // exp2(-inf) = 0
-        c_s[h] = c;
-        l_s[h] = l_s[h] * c + sum;
-        m_s[h] = m_new;
-      }
+    // sum over the OCT lanes of the token (uniform branches on OCT)
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1)
+      if (OCT > off)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int h = 0; h < HB; ++h) s[u][h] = add_partner(s[u][h], off);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = token(k0 + u) < t1;
+#pragma unroll
+      for (int h = 0; h < HB; ++h) s[u][h] = valid ? s[u][h] * bt.ks[u] : -INFINITY;
     }
-    __syncthreads();
-    // ---- P.V
+    float m_ref[HB];
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
-      const float c = h < nh ? c_s[h] : 0.f;
+      float mx = s[0][h];
+#pragma unroll
+      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][h]);
+      const float m_new = fmaxf(m[h], mx);
+      m_ref[h] = m_new == -INFINITY ? 0.f : m_new;
+      const float c = __builtin_amdgcn_exp2f(m[h] - m_ref[h]);  // exp2(-inf) = 0
+      l[h] *= c;
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[h][i] *= c;
+      m[h] = m_new;
     }
-    if (dact) {
-      for (int j = tsub; j < n; j += nsub) {
-        const int8_t *vp = vc + (base + tt + j) * (size_t)D + d0;
-        const float vsc = sf_load_as_f32<SDT>(vs, base + tt + j);
-        float vf[8];
-        if (d0 + 8 <= D) {
-          const uint64_t vv = *(const uint64_t *)vp;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) vf[i] = (float)(int8_t)(vv >> (8 * i)) * vsc;
-        } else {
+    for (int u = 0; u < U; ++u) {
+      float vf[8];
+      i8x8_to_f32(bt.v[u], vf);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) vf[i] = d0 + i < D ? (float)vp[i] * vsc : 0.f;
-        }
+      for (int h = 0; h < HB; ++h) {
+        const float p = __builtin_amdgcn_exp2f(s[u][h] - m_ref[h]);
+        l[h] += p;
+        const float pv = p * bt.vs[u];  // the V scale folded into P
 #pragma unroll
-        for (int h = 0; h < HB; ++h) {
-          if (h < nh) {
-            const float p = sc[h][j];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
-          }
-        }
+        for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pv, vf[i], acc[h][i]);
       }
     }
-    __syncthreads();
+  };
+
+  if (nsteps > 0) {
+    // loads are unconditional (past the end they re-read the last token) so
+    // the next batch stays in flight while the current one is computed
+    Batch b0, b1;
+    load(0, b0);
+    for (int k0 = 0; k0 < nsteps; k0 += 2 * U) {
+      load(k0 + U, b1);
+      compute(k0, b0);
+      if (k0 + U >= nsteps) break;
+      load(k0 + 2 * U, b0);
+      compute(k0 + U, b1);
+    }
   }
 
-  // ---- reduce acc over the token sub-lanes: in-wave, then across waves
-  for (int off = 32; off >= tpt; off >>= 1)
+  // ---- merge the NS lane states of each head (LDS)
+  float *accs = smem;               // [NS][HB][D]
+  float *ms = accs + NS * HB * D;   // [NS][HB]: m, then the state weights
+  float *ls = ms + NS * HB;         // [NS][HB]
+  float *Ms = ls + NS * HB, *Ls = Ms + HB;
 #pragma unroll
-    for (int h = 0; h < HB; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] += sf_shfl_xor(acc[h][i], off);
-  if (lane < tpt && dact) {
-#pragma unroll
-    for (int h = 0; h < HB; ++h)
-      if (h < nh)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (d0 + i < D) red[((size_t)wave * HB + h) * D + d0 + i] = acc[h][i];
+  for (int h = 0; h < HB; ++h) {
+    if (h < nh && dact) {
+      float4_t *dst = (float4_t *)(accs + ((size_t)slot * HB + h) * D + d0);
+      dst[0] = float4_t{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+      dst[1] = float4_t{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+    }
+    if (h < nh && oct == 0) {
+      ms[slot * HB + h] = m[h];
+      ls[slot * HB + h] = l[h];
+    }
   }
   __syncthreads();
-  const int nw = kAttnThreads / 64;
-  for (int idx = tid; idx < nh * D; idx += kAttnThreads) {
-    const int h = idx / D, d = idx - h * D;
-    float s = 0.f;
-    for (int w = 0; w < nw; ++w) s += red[((size_t)w * HB + h) * D + d];
-    const size_t bh = (size_t)b * H + (size_t)kvh * G + h0 + h;
-    part_acc[(bh * n_splits + split) * D + d] = s;
+  // state weights: 32 lanes per head, lane j covering states j, j + 32, ...
+  {
+    const int h = tid >> 5, j = tid & 31;
+    const bool on = h < nh;
+    float mx = -INFINITY;
+    if (on)
+      for (int s = j; s < NS; s += 32) mx = fmaxf(mx, ms[s * HB + h]);
+    const float M = group32_max(mx);
+    const float M_ref = M == -INFINITY ? 0.f : M;
+    float lsum = 0.f;
+    if (on)
+      for (int s = j; s < NS; s += 32) {
+        const float w = __builtin_amdgcn_exp2f(ms[s * HB + h] - M_ref);
+        ms[s * HB + h] = w;
+        lsum = fmaf(w, ls[s * HB + h], lsum);
+      }
+    lsum = group32_sum(lsum);
+    if (on && j == 0) {
+      Ms[h] = M;
+      Ls[h] = lsum;
+    }
   }
-  if (tid < nh) {
-    const size_t bh = (size_t)b * H + (size_t)kvh * G + h0 + tid;
-    part_ml[(bh * n_splits + split) * 2 + 0] = m_s[tid];
-    part_ml[(bh * n_splits + split) * 2 + 1] = l_s[tid];
-  }
-}
-
-// Merge the split partials of one (b, h): M = max m_s, c_s = 2^(m_s - M),
-// out = sum_s c_s acc_s / max(sum_s c_s l_s, 1e-20) (q4_attention.py:256-261).
-// The block first reduces M and L over the splits in parallel, keeps c_s in
-// LDS, then (dim, split-slice) threads sum their slice and fold through LDS.
-constexpr int kCombineThreads = 256;
-constexpr int kMaxSplits = 2048;
-
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float *scratch) {
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = sf_shfl_xor(v, off);
-    v = is_max ? fmaxf(v, o) : v + o;
-  }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  v = scratch[0];
-  for (int w = 1; w < kCombineThreads / 64; ++w) v = is_max ? fmaxf(v, scratch[w]) : v + scratch[w];
-  return v;
-}
-
-__global__ void __launch_bounds__(kCombineThreads)
-k_attn_combine(const float *__restrict__ part_acc, const float *__restrict__ part_ml,
-               void *__restrict__ out, int odt, int D, int n_splits) {
-  __shared__ float c_s[kMaxSplits];
-  __shared__ float scratch[kCombineThreads / 64];
-  __shared__ float fold[kCombineThreads];
-  const size_t bh = blockIdx.x;
-  const int tid = threadIdx.x;
-  const float *ml = part_ml + bh * n_splits * 2;
-  float mx = -INFINITY;
-  for (int s = tid; s < n_splits; s += kCombineThreads) mx = fmaxf(mx, ml[2 * s]);
-  const float M = block_reduce(mx, true, scratch);
-  float lsum = 0.f;
-  for (int s = tid; s < n_splits; s += kCombineThreads) {
-    const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[2 * s] - M);
-    c_s[s] = c;
-    lsum = fmaf(ml[2 * s + 1], c, lsum);
-  }
-  const float L = block_reduce(lsum, false, scratch);  // also orders the c_s writes
-  const float inv = 1.f / fmaxf(L, 1e-20f);
-  // dims over lanes, splits over slices
-  const int nslice = kCombineThreads / D > 0 ? kCombineThreads / D : 1;
-  const int d = tid % D, slice = tid / D;
-  float a = 0.f;
-  if (slice < nslice && d < D) {
-    const float *pa = part_acc + bh * n_splits * D + d;
+  const bool single = n_splits == 1;
+  const int nq = D >> 2;
+  for (int it = tid; it < nh * nq; it += NT) {
+    const int h = it / nq, dq4 = (it - h * nq) * 4;
+    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll 4
-    for (int s = slice; s < n_splits; s += nslice) a = fmaf(pa[(size_t)s * D], c_s[s], a);
+    for (int s = 0; s < NS; s += 2) {  // NS is a multiple of 4
+      a0 += *(const float4_t *)(accs + ((size_t)s * HB + h) * D + dq4) * ms[s * HB + h];
+      a1 += *(const float4_t *)(accs + ((size_t)(s + 1) * HB + h) * D + dq4) * ms[(s + 1) * HB + h];
+    }
+    const float4_t a = a0 + a1;
+    if (single) {
+      const float L = Ls[h];
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const size_t o = (bh0 + h) * D + dq4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = a[i] * inv;
+        if (odt == SF_F32) ((float *)out)[o + i] = v;
+        else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
+        else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
+      }
+    } else {
+      float *pa = part_acc + ((bh0 + h) * n_splits + split) * D + dq4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st_agent(pa + i, a[i]);
+    }
   }
-  fold[tid] = a;
+  if (single) return;
+  if (tid < nh) {
+    st_agent(part_ml + ((bh0 + tid) * n_splits + split) * 2 + 0, Ms[tid]);
+    st_agent(part_ml + ((bh0 + tid) * n_splits + split) * 2 + 1, Ls[tid]);
+  }
+
+  // ---- the last split of this (b, kv head, head block) merges all partials
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
-  for (int dd = tid; dd < D; dd += kCombineThreads) {
-    float v = 0.f;
-    for (int sl = 0; sl < nslice; ++sl) v += fold[sl * D + dd];
-    v *= inv;
-    if (odt == SF_F32) ((float *)out)[bh * D + dd] = v;
-    else if (odt == SF_F16) ((f16 *)out)[bh * D + dd] = (f16)v;
-    else ((uint16_t *)out)[bh * D + dd] = sf_f32_to_bf16(v);
+  unsigned *ctr = counters + ((size_t)b * KVH + kvh) * n_hblk + hblk;
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(n_splits - 1);
   }
+  __syncthreads();
+  if (!s_last) return;
+
+  // Partials of (head, 4-dim quad) items; with fewer items than threads the
+  // splits are cut into nsl slices whose sums are folded through LDS. Each
+  // thread's first kMergeChunk partials are loaded before the (m, l) staging
+  // so that all loads of the merge are in flight together.
+  float4_t *red4 = (float4_t *)smem;        // [NT]
+  float *cw = smem + 4 * NT;                // [HB][kMaxSplits]: m, then weights
+  float *cl = cw + HB * kMaxSplits;         // [HB][kMaxSplits]: l
+  float *Lg = cl + HB * kMaxSplits;         // [HB]
+  const int items = nh * nq;
+  const int nsl = items >= NT ? 1 : NT / items;
+  const int units = items * nsl;            // (item, slice) pairs
+  auto part4 = [&](int item, int s) {
+    const int h = item / nq, dqq = (item - h * nq) * 4;
+    const float *pp = part_acc + ((bh0 + h) * n_splits + s) * D + dqq;
+    const float2_t lo = ld2_agent(pp), hi = ld2_agent(pp + 2);
+    return float4_t{lo.x, lo.y, hi.x, hi.y};
+  };
+  constexpr int CH = kMergeChunk;
+  float4_t pre[CH];
+  {
+    const int unit = tid < units ? tid : 0;
+    const int item = unit % items, sl = unit / items;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) pre[j] = part4(item, min(sl + j * nsl, n_splits - 1));
+  }
+  // split weights: 32 lanes per head, lane j covering splits j, j + 32, ...
+  {
+    const int h = tid >> 5, j = tid & 31;
+    const bool on = h < nh;
+    const float *mlh = part_ml + (bh0 + (on ? h : 0)) * n_splits * 2;
+    // the first two are loaded unconditionally (clamped) to keep them in flight together
+    const float2_t ml0 = ld2_agent(mlh + 2 * min(j, n_splits - 1));
+    const float2_t ml1 = ld2_agent(mlh + 2 * min(j + 32, n_splits - 1));
+    float mx = -INFINITY;
+    if (on) {
+      if (j < n_splits) {
+        cw[h * kMaxSplits + j] = ml0.x;
+        cl[h * kMaxSplits + j] = ml0.y;
+        mx = ml0.x;
+      }
+      if (j + 32 < n_splits) {
+        cw[h * kMaxSplits + j + 32] = ml1.x;
+        cl[h * kMaxSplits + j + 32] = ml1.y;
+        mx = fmaxf(mx, ml1.x);
+      }
+      for (int s = j + 64; s < n_splits; s += 32) {
+        const float2_t ml = ld2_agent(mlh + 2 * s);
+        cw[h * kMaxSplits + s] = ml.x;
+        cl[h * kMaxSplits + s] = ml.y;
+        mx = fmaxf(mx, ml.x);
+      }
+    }
+    const float M = group32_max(mx);
+    const float M_ref = M == -INFINITY ? 0.f : M;
+    float lsum = 0.f;
+    if (on)
+      for (int s = j; s < n_splits; s += 32) {
+        const float w = __builtin_amdgcn_exp2f(cw[h * kMaxSplits + s] - M_ref);
+        cw[h * kMaxSplits + s] = w;
+        lsum = fmaf(cl[h * kMaxSplits + s], w, lsum);
+      }
+    lsum = group32_sum(lsum);
+    if (on && j == 0) Lg[h] = lsum;
+  }
+  __syncthreads();
+  auto unit_sum = [&](int unit, bool first) {
+    const int item = unit % items, sl = unit / items, h = item / nq;
+    const float *w = cw + h * kMaxSplits;
+    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    int j0 = 0;
+    if (first) {
+#pragma unroll
+      for (int j = 0; j < CH; j += 2) {
+        const int s0 = sl + j * nsl, s1 = s0 + nsl;
+        a0 += pre[j] * (s0 < n_splits ? w[s0] : 0.f);
+        a1 += pre[j + 1] * (s1 < n_splits ? w[s1] : 0.f);
+      }
+      j0 = CH;
+    }
+    for (int s = sl + j0 * nsl; s < n_splits; s += nsl) a0 += part4(item, s) * w[s];
+    return a0 + a1;
+  };
+  auto write_item = [&](int item, float4_t a) {
+    const int h = item / nq, dqq = (item - h * nq) * 4;
+    const float L = Lg[h];
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const size_t o = (bh0 + h) * D + dqq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = a[i] * inv;
+      if (odt == SF_F32) ((float *)out)[o + i] = v;
+      else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
+      else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
+    }
+  };
+  if (nsl == 1) {
+    for (int item = tid; item < items; item += NT) write_item(item, unit_sum(item, item == tid));
+  } else {
+    if (tid < units) red4[tid] = unit_sum(tid, true);
+    __syncthreads();
+    if (tid < items) {
+      float4_t a = red4[tid];
+      for (int k = 1; k < nsl; ++k) a += red4[k * items + tid];
+      write_item(tid, a);
+    }
+  }
+  if (tid == 0)  // ready for the next call on this workspace
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int pow2_log2_at_least(int v) {
@@ -345,6 +538,8 @@ extern "C" int sf_kv_quant_append(const void *k_new, const void *v_new, int in_d
              D);
   SF_REQUIRE(k_new && v_new && k_codes && k_scales && v_codes && v_scales, SF_EINVAL,
              "null pointer argument");
+  SF_REQUIRE((((uintptr_t)k_codes | (uintptr_t)v_codes) & 7) == 0, SF_EINVAL,
+             "KV code buffers must be 8-byte aligned");
   SF_REQUIRE(in_dtype >= SF_F32 && in_dtype <= SF_BF16, SF_EINVAL, "bad input dtype %d", in_dtype);
   SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
              scale_dtype);
@@ -371,20 +566,43 @@ extern "C" int sf_kv_quant_append(const void *k_new, const void *v_new, int in_d
   return sf_check_launch("sf_kv_quant_append");
 }
 
+// Workspace: a fixed 16 KiB region of uint32 counters (one per (b, kv head,
+// head block) of a call), then partial acc [B*H][S][D] fp32, then (m, l)
+// [B*H][S][2]. The counters sit at the same place for every shape, so one
+// zero-filled workspace serves calls of any shape: each call's last split
+// resets the counter it used.
+constexpr size_t kCounterBytes = 16384;
+constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(unsigned));
+
+static size_t attn_ws_parts(int B, int H, int D, int S, size_t *acc_off, size_t *ml_off) {
+  const size_t rows = (size_t)B * H * S;
+  *acc_off = kCounterBytes;
+  *ml_off = sf_align256(*acc_off + rows * D * sizeof(float));
+  return *ml_off + rows * 2 * sizeof(float);
+}
+
 extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
   if (B <= 0 || H <= 0 || D <= 0 || n_splits <= 0) return 0;
-  const size_t rows = (size_t)B * H * n_splits;
-  return sf_align256(rows * D * sizeof(float)) + rows * 2 * sizeof(float);
+  if (n_splits > kMaxSplits) n_splits = kMaxSplits;
+  size_t acc_off, ml_off;
+  return attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
 }
 
 extern "C" int sf_attn_default_splits(int B, int KVH, int T) {
-  // Enough (split, kv head, b) workgroups to cover the 256 CUs about twice,
-  // without tiles shorter than one 64-token sub-tile.
-  if (B <= 0 || KVH <= 0 || T <= 0) return 1;
-  const int want = (512 + B * KVH - 1) / (B * KVH);
-  const int cap = (T + kSubTile - 1) / kSubTile;
-  int s = want < cap ? want : cap;
+  // About 128 tokens per split (one batch of 4 rows per wave at head_dim
+  // 64), at most 64 splits so that the final merge's loads of the partials
+  // all go out at once. Measured on MI355X at B = 1, 2 kv heads: 32 splits
+  // for T = 4096 and 64 for T = 16384 are the fastest of 1..128.
+  (void)B;
+  (void)KVH;
+  if (T <= 0) return 1;
+  int s = (T + 127) / 128;
+  if (s > 64) s = 64;
   return s < 1 ? 1 : s;
+}
+
+static int attn_heads_per_block(int G) {
+  return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 6 ? 6 : G <= 7 ? 7 : 8;
 }
 
 extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
@@ -396,7 +614,7 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
   SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
              "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
   SF_REQUIRE(H % KVH == 0, SF_EINVAL, "n_heads=%d not a multiple of n_kv_heads=%d", H, KVH);
-  SF_REQUIRE(D <= 256, SF_EINVAL, "head_dim=%d exceeds kernel's compile-time max 256", D);
+  SF_REQUIRE(D <= kMaxD, SF_EINVAL, "head_dim=%d exceeds kernel's compile-time max 256", D);
   SF_REQUIRE(D % 8 == 0, SF_EUNSUPPORTED, "head_dim=%d: need a multiple of 8", D);
   SF_REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out && workspace, SF_EINVAL,
              "null pointer argument");
@@ -404,6 +622,10 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
              SF_EINVAL, "bad q/out dtype");
   SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
              scale_dtype);
+  SF_REQUIRE(((uintptr_t)workspace & 255) == 0, SF_EINVAL, "workspace must be 256-byte aligned");
+  SF_REQUIRE((((uintptr_t)k_codes | (uintptr_t)v_codes) & 7) == 0, SF_EINVAL,
+             "KV code buffers must be 8-byte aligned");
+  SF_REQUIRE(((uintptr_t)q & 15) == 0, SF_EINVAL, "q must be 16-byte aligned");
   if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T);
   // the reference's tiling: n_tiles = max(1, min(n_tiles, T)); tile = ceil(T / n_tiles)
   n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
@@ -413,32 +635,44 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
   const size_t need = sf_attn_workspace_bytes(B, H, D, n_splits);
   SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "attention workspace too small: %zu < %zu",
              workspace_bytes, need);
-  float *part_acc = (float *)workspace;
-  float *part_ml =
-      (float *)((char *)workspace + sf_align256((size_t)B * H * n_splits * D * sizeof(float)));
+  size_t acc_off, ml_off;
+  attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
+  float *part_acc = (float *)((char *)workspace + acc_off);
+  float *part_ml = (float *)((char *)workspace + ml_off);
+  unsigned *counters = (unsigned *)workspace;
   const int G = H / KVH;
-  const int n_hblk = (G + kHeadsPerBlock - 1) / kHeadsPerBlock;
-  const int tpt_log2 = pow2_log2_at_least(D / 8);
+  const int HB = attn_heads_per_block(G);
+  const int n_hblk = (G + HB - 1) / HB;
+  SF_REQUIRE(B * KVH * n_hblk <= kMaxCounters, SF_EUNSUPPORTED,
+             "attention batch too large for one call (B * n_kv_heads * head blocks = %d > %d)",
+             B * KVH * n_hblk, kMaxCounters);
+  const int oct_log2 = pow2_log2_at_least(D / 8);
   const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
   dim3 grid(n_splits, KVH * n_hblk, B);
-  const size_t shm = (size_t)(kAttnThreads / 64) * kHeadsPerBlock * D * sizeof(float);
   hipStream_t st = (hipStream_t)stream;
-#define SF_ATTN_LAUNCH(QD, SD)                                                                  \
-  k_attn_split<QD, SD><<<grid, kAttnThreads, shm, st>>>(q, k_codes, k_scales, v_codes, v_scales, \
-                                                         part_acc, part_ml, H, KVH, T, T_cap, D, \
-                                                         qscale, n_splits, tile, tpt_log2)
+#define SF_ATTN_LAUNCH(QD, SD, HBV)                                                            \
+  k_attn_decode<QD, SD, HBV><<<grid, kAttnThreads, 0, st>>>(                                   \
+      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H, \
+      KVH, T, T_cap, D, qscale, n_splits, tile, oct_log2)
+#define SF_ATTN_HB(QD, SD)                       \
+  do {                                           \
+    if (HB == 1) SF_ATTN_LAUNCH(QD, SD, 1);      \
+    else if (HB == 2) SF_ATTN_LAUNCH(QD, SD, 2); \
+    else if (HB == 4) SF_ATTN_LAUNCH(QD, SD, 4); \
+    else if (HB == 6) SF_ATTN_LAUNCH(QD, SD, 6); \
+    else if (HB == 7) SF_ATTN_LAUNCH(QD, SD, 7); \
+    else SF_ATTN_LAUNCH(QD, SD, 8);              \
+  } while (0)
   if (scale_dtype == SF_F16) {
-    if (q_dtype == SF_F32) SF_ATTN_LAUNCH(SF_F32, SF_F16);
-    else if (q_dtype == SF_F16) SF_ATTN_LAUNCH(SF_F16, SF_F16);
-    else SF_ATTN_LAUNCH(SF_BF16, SF_F16);
+    if (q_dtype == SF_F32) SF_ATTN_HB(SF_F32, SF_F16);
+    else if (q_dtype == SF_F16) SF_ATTN_HB(SF_F16, SF_F16);
+    else SF_ATTN_HB(SF_BF16, SF_F16);
   } else {
-    if (q_dtype == SF_F32) SF_ATTN_LAUNCH(SF_F32, SF_F32);
-    else if (q_dtype == SF_F16) SF_ATTN_LAUNCH(SF_F16, SF_F32);
-    else SF_ATTN_LAUNCH(SF_BF16, SF_F32);
+    if (q_dtype == SF_F32) SF_ATTN_HB(SF_F32, SF_F32);
+    else if (q_dtype == SF_F16) SF_ATTN_HB(SF_F16, SF_F32);
+    else SF_ATTN_HB(SF_BF16, SF_F32);
   }
+#undef SF_ATTN_HB
 #undef SF_ATTN_LAUNCH
-  int rc = sf_check_launch("sf_attn_decode_i8kv(split)");
-  if (rc) return rc;
-  k_attn_combine<<<B * H, kCombineThreads, 0, st>>>(part_acc, part_ml, out, out_dtype, D, n_splits);
-  return sf_check_launch("sf_attn_decode_i8kv(combine)");
+  return sf_check_launch("sf_attn_decode_i8kv");
 }

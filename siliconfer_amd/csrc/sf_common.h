@@ -98,6 +98,33 @@ __device__ __forceinline__ float sf_load_as_f32(const void *p, size_t i) {
   else return sf_bf16_to_f32(((const uint16_t *)p)[i]);
 }
 
+// 8 contiguous elements starting at element i (i a multiple of 8, p 16-byte
+// aligned) with 16-byte loads
+template <int DT>
+__device__ __forceinline__ void sf_load8_as_f32(const void *p, size_t i, float (&f)[8]) {
+  if constexpr (DT == SF_F32) {
+    const float4_t a = ((const float4_t *)p)[i / 4], b = ((const float4_t *)p)[i / 4 + 1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[j] = a[j];
+      f[4 + j] = b[j];
+    }
+  } else {
+    const u32x4 w = ((const u32x4 *)p)[i / 8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = w[j];
+      if constexpr (DT == SF_F16) {
+        f[2 * j] = (float)sf_bitcast<f16>((uint16_t)(x & 0xffffu));
+        f[2 * j + 1] = (float)sf_bitcast<f16>((uint16_t)(x >> 16));
+      } else {
+        f[2 * j] = sf_bitcast<float>(x << 16);
+        f[2 * j + 1] = sf_bitcast<float>(x & 0xffff0000u);
+      }
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void sf_store_from_f32(void *p, size_t i, float v) {
   if constexpr (DT == SF_F32) ((float *)p)[i] = v;

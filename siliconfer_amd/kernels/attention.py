@@ -35,6 +35,20 @@ def default_splits(B: int, n_kv_heads: int, T: int) -> int:
     return int(_lib.load().sf_attn_default_splits(B, n_kv_heads, T))
 
 
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
+    """Zero-filled attention workspace, one per (device, stream), grown on demand.
+    The kernel leaves its counters at zero after every call, so it is reused."""
+    key = (device, stream_handle)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
 def attention_decode(q: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Tensor,
                      v_codes: torch.Tensor, v_scales: torch.Tensor, T: int | None = None,
                      n_splits: int | None = None, scale: float | None = None,
@@ -70,15 +84,16 @@ def attention_decode(q: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Ten
     lib = _lib.load()
     if n_splits is None or n_splits <= 0:
         n_splits = int(lib.sf_attn_default_splits(B, KVH, T))
-    n_splits = max(1, min(int(n_splits), max(T, 1)))
+    n_splits = max(1, min(int(n_splits), max(T, 1), 512))
     ws_bytes = lib.sf_attn_workspace_bytes(B, H, D, n_splits)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    st = _lib.stream(q)
+    ws = workspace(q.device, st, ws_bytes)
     if out is None:
         out = torch.empty((B, H, D), dtype=out_dtype, device=q.device)
     rc = lib.sf_attn_decode_i8kv(q.data_ptr(), _lib.dt(q), k_codes.data_ptr(), ks.data_ptr(),
                                  v_codes.data_ptr(), vs.data_ptr(), _lib.dt(ks), out.data_ptr(),
-                                 _lib.dt(out), ws.data_ptr(), ws_bytes, B, H, KVH, T, T_cap, D,
-                                 float(scale), n_splits, _lib.stream(q))
+                                 _lib.dt(out), ws.data_ptr(), ws.numel(), B, H, KVH, T, T_cap, D,
+                                 float(scale), n_splits, st)
     _lib.check(rc, "sf_attn_decode_i8kv")
     return out
 

@@ -83,15 +83,17 @@ def test_gemm_workspace_and_validation():
 
 def test_attention_validation_and_sizes():
     lib = _lib.load()
-    assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == 14 * 256 * 64 * 4 + 14 * 256 * 2 * 4
+    acc = 14 * 256 * 64 * 4
+    assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == 16384 + acc + 14 * 256 * 2 * 4
     rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
                                  1, 14, 2, 16, 16, 512, 0.1, 1, None)
     assert rc == -1 and "exceeds kernel's compile-time max 256" in _lib.last_error()
     rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
                                  1, 14, 3, 16, 16, 64, 0.1, 1, None)
     assert rc == -1 and "not a multiple" in _lib.last_error()
-    assert lib.sf_attn_default_splits(1, 2, 16384) == 256
-    assert lib.sf_attn_default_splits(1, 2, 100) == 2
+    assert lib.sf_attn_default_splits(1, 2, 16384) == 64
+    assert lib.sf_attn_default_splits(1, 2, 4096) == 32
+    assert lib.sf_attn_default_splits(1, 2, 100) == 1
 
 
 def test_kv_append_validation():

@@ -129,3 +129,59 @@ def test_head_group_larger_than_block(dev):
     """GQA groups of more than 8 query heads span several head blocks."""
     rng = np.random.default_rng(22)
     check(dev, *make_inputs(rng, 2, 20, 2, 64, 150), what="G=10")
+
+
+def test_max_splits(dev):
+    """512 splits (the kernel's maximum) over a 4096-token cache."""
+    rng = np.random.default_rng(23)
+    check(dev, *make_inputs(rng, 1, 14, 2, 64, 4096), n_tiles=512, what="512 splits")
+
+
+def test_workspace_reused_across_shapes(dev):
+    """One zero-filled workspace serves calls of different shapes in a row: each
+    call leaves the merge counters (first 16 KiB) back at zero."""
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    t = lambda a: torch.as_tensor(a).to(dev).contiguous()
+    cases = [(2, 20, 2, 64, 1000, 300), (1, 14, 2, 64, 100, 7), (2, 20, 2, 64, 1000, 300),
+             (1, 8, 8, 128, 333, 64)]
+    for i, (B, H, KVH, D, T, S) in enumerate(cases):
+        rng = np.random.default_rng(100 + i)
+        q, kc, ks, vc, vs = make_inputs(rng, B, H, KVH, D, T)
+        out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+        qd, kcd, ksd, vcd, vsd = t(q), t(kc), t(ks), t(vc), t(vs)
+        assert lib.sf_attn_workspace_bytes(B, H, D, S) <= ws.numel()
+        rc = lib.sf_attn_decode_i8kv(qd.data_ptr(), _lib.SF_F32, kcd.data_ptr(), ksd.data_ptr(),
+                                     vcd.data_ptr(), vsd.data_ptr(), _lib.SF_F32, out.data_ptr(),
+                                     _lib.SF_F32, ws.data_ptr(), ws.numel(), B, H, KVH, T, T, D,
+                                     float(D ** -0.5), S, st)
+        _lib.check(rc, "sf_attn_decode_i8kv")
+        torch.cuda.synchronize()
+        assert int(ws[:16384].count_nonzero()) == 0, f"counters left set after case {i}"
+        ref = A.attention_decode(q, kc, ks, vc, vs)
+        assert_close(out.cpu().numpy(), ref, TOL, f"case {i}")
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float16, 2e-3), (torch.bfloat16, 8e-3)])
+def test_half_precision_q_and_out(dev, dtype, tol):
+    """q and the output in fp16 / bf16; the tolerance adds the output's own
+    rounding (bf16 keeps 8 significant bits)."""
+    rng = np.random.default_rng(24)
+    q, kc, ks, vc, vs = make_inputs(rng, 1, 14, 2, 64, 700)
+    qh = torch.as_tensor(q).to(dtype)
+    t = lambda a: torch.as_tensor(a).to(dev)
+    out = attention_decode(qh.to(dev), t(kc), t(ks), t(vc), t(vs), out_dtype=dtype)
+    assert out.dtype == dtype
+    ref = A.attention_decode(qh.float().numpy().astype(np.float64), kc, ks, vc, vs)
+    assert_close(out.float().cpu().numpy(), ref, tol, f"{dtype}")
+
+
+@pytest.mark.parametrize("G", [3, 5, 6, 7, 8, 12, 16])
+def test_gqa_group_widths(dev, G):
+    """Every head-block width the kernel is built for (exact and padded blocks,
+    and groups split over several blocks)."""
+    rng = np.random.default_rng(30 + G)
+    check(dev, *make_inputs(rng, 2, 2 * G, 2, 64, 333), what=f"G={G}")
