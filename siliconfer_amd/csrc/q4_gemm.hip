@@ -16,9 +16,12 @@
 // (fp16 exactly, fp32 to ~16 bits) and all four products are accumulated, so
 // fp16 activations give exact products like the bf16 ones.
 //
-// Tiling: 128 x 128 output tile per 256-thread workgroup (2 x 2 waves, each
-// 64 x 64 = 2 x 2 MFMA 32x32 tiles), K steps of 64 staged through padded LDS
-// rows, next step's global loads issued before the current step's MFMAs. When
+// Tiling: 128 x 128 output tile per 512-thread workgroup (2 x 4 waves, each
+// 64 x 32 = 2 MFMA 32x32 tiles; two waves per SIMD), K steps of 64 staged
+// through two padded LDS buffers; each step's global loads are issued three
+// steps ahead (a ring of three register stages) so HBM latency hides behind
+// the MFMAs. The output tile goes back through LDS so that stores are whole
+// row segments. When
 // the tile grid is too small to fill the GPU, K is split across workgroups
 // into an fp32 workspace and summed by a second kernel in a fixed order.
 #include "sf_common.h"
@@ -30,28 +33,37 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row (+16 B breaks bank conflicts)
-constexpr int NTHREADS = 256;
+constexpr int NTHREADS = 512;      // 8 waves: two per SIMD, so one's VALU overlaps another's MFMA
+constexpr int KPT = BM * BK / NTHREADS;  // 16 elements of X (and of W) staged per thread per step
+constexpr int WAVE_M = 64, WAVE_N = 32;  // wave tile: 2 x 1 MFMA 32x32 tiles
+constexpr int OUT_PITCH = WAVE_N + 4;    // fp32 pitch of a wave's output tile staged in LDS
+static_assert(BN * BK / NTHREADS == KPT, "X and W staging shares must match");
+static_assert((BM / WAVE_M) * (BN / WAVE_N) * 64 == NTHREADS, "wave grid must cover the tile");
 
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
   // top 16 bits of a (low half) and of b (high half)
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-// One thread's share of the X tile: row tid/2, 32 consecutive k starting at
-// 32*(tid%2). Loaded into registers as raw bits.
+// One thread's share of the X tile: row tid/4, KPT consecutive k starting at
+// KPT*(tid%4). Loaded into registers as raw bits; loads are unconditional
+// (clamped in-bounds address; K is a multiple of 32) so they stay in flight,
+// and rows or k past the end are zeroed when the registers are staged.
 template <int XDT>
 struct XRegs {
-  static constexpr int NQ = XDT == SF_F32 ? 8 : 4;  // 16-byte loads
+  static constexpr int NQ = KPT * (XDT == SF_F32 ? 4 : 2) / 16;  // 16-byte loads
   u32x4 v[NQ];
+  bool ok;
 };
 
 template <int XDT>
 __device__ __forceinline__ void load_x(XRegs<XDT> &r, const void *X, int M, int K, int m, int k) {
-  const bool ok = m < M && k < K;
+  r.ok = m < M && k < K;
   const size_t esz = XDT == SF_F32 ? 4 : 2;
-  const u32x4 *p = (const u32x4 *)((const char *)X + ((size_t)m * K + k) * esz);
+  const u32x4 *p =
+      (const u32x4 *)((const char *)X + ((size_t)min(m, M - 1) * K + min(k, K - KPT)) * esz);
 #pragma unroll
-  for (int i = 0; i < XRegs<XDT>::NQ; ++i) r.v[i] = ok ? p[i] : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < XRegs<XDT>::NQ; ++i) r.v[i] = p[i];
 }
 
 // Split 2 fp32 values into (hi pair, lo pair) of bf16: hi = truncation, lo = rest.
@@ -64,29 +76,30 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
   lo = hi_pair(sf_bitcast<uint32_t>(ra), sf_bitcast<uint32_t>(rb));
 }
 
-// Write the thread's 32 activations to the LDS tiles (hi only for bf16).
+// Write the thread's KPT activations to the LDS tiles (hi only for bf16).
 template <int XDT>
 __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, uint16_t *xs_lo,
                                         int lrow, int lk) {
   u32x4 *dh = (u32x4 *)(xs_hi + lrow * LDS_PITCH + lk);
+  const uint32_t keep = r.ok ? 0xFFFFFFFFu : 0u;
   if constexpr (XDT == SF_BF16) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dh[i] = r.v[i];
+    for (int i = 0; i < KPT / 8; ++i) dh[i] = r.v[i] & keep;
   } else {
     u32x4 *dl = (u32x4 *)(xs_lo + lrow * LDS_PITCH + lk);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // 8 activations per 16-byte LDS store
+    for (int i = 0; i < KPT / 8; ++i) {  // 8 activations per 16-byte LDS store
       float f[8];
       if constexpr (XDT == SF_F16) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const half2_t h = sf_bitcast<half2_t>(r.v[i][j]);
+          const half2_t h = sf_bitcast<half2_t>(r.v[i][j] & keep);
           f[2 * j] = (float)h.x;
           f[2 * j + 1] = (float)h.y;
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = sf_bitcast<float>(r.v[2 * i + j / 4][j % 4]);
+        for (int j = 0; j < 8; ++j) f[j] = sf_bitcast<float>(r.v[2 * i + j / 4][j % 4] & keep);
       }
       u32x4 h4, l4;
 #pragma unroll
@@ -102,45 +115,49 @@ __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, ui
   }
 }
 
-// One thread's share of the W tile: 16 bytes (32 nibbles) of row n at k.
+// One thread's share of the W tile: 8 bytes (KPT = 16 nibbles) of row n at k,
+// and the raw scale / zero-point bits of that (row, group); converted at
+// staging (a step never straddles a group: g is a multiple of 32 and KPT
+// divides 32).
 struct WRegs {
-  u32x4 w;
-  float s, zs;  // scale and z*scale
+  u32x2 w;
+  uint32_t sbits, zbyte;
+  bool ok;
 };
 
+template <bool ASYM>
 __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *__restrict__ wq,
                                        const f16 *__restrict__ st, const uint8_t *__restrict__ zt,
                                        int N, int K, int G, int g, int n, int k) {
-  if (n < N && k < K) {
-    r.w = *(const u32x4 *)(wq + (size_t)n * (K >> 1) + (k >> 1));
-    const int grp = k / g;
-    const size_t cell = (size_t)(n >> 3) * G + grp;
-    const float s = (float)st[cell * 8 + (n & 7)];
-    uint32_t z = 8u;  // offset-binary symmetric codes
-    if (zt) z = (zt[cell * 4 + ((n & 7) >> 1)] >> (4 * (n & 1))) & 15u;
-    r.s = s;
-    r.zs = (float)z * s;
-  } else {
-    r.w = u32x4{0u, 0u, 0u, 0u};
-    r.s = 0.f;
-    r.zs = 0.f;
-  }
+  r.ok = n < N && k < K;
+  const int nc = min(n, N - 1), kc = min(k, K - KPT);
+  r.w = *(const u32x2 *)(wq + (size_t)nc * (K >> 1) + (kc >> 1));
+  const size_t cell = (size_t)(nc >> 3) * G + kc / g;
+  r.sbits = ((const uint16_t *)st)[cell * 8 + (nc & 7)];
+  if constexpr (ASYM) r.zbyte = zt[cell * 4 + ((nc & 7) >> 1)];
 }
 
-// Dequantize 32 weights exactly and store them as bf16 hi / lo LDS rows.
+// Dequantize KPT weights exactly and store them as bf16 hi / lo LDS rows.
+template <bool ASYM>
 __device__ __forceinline__ void store_w(const WRegs &r, uint16_t *ws_hi, uint16_t *ws_lo, int lrow,
                                         int lk) {
   u32x4 *dh = (u32x4 *)(ws_hi + lrow * LDS_PITCH + lk);
   u32x4 *dl = (u32x4 *)(ws_lo + lrow * LDS_PITCH + lk);
+  // row n's zero-point nibble: the low one for even n, the high one for odd n
+  // (offset-binary symmetric codes have z = 8)
+  uint32_t z = 8u;
+  if constexpr (ASYM) z = (r.zbyte >> (4 * (lrow & 1))) & 15u;
+  const float sc = r.ok ? (float)sf_bitcast<f16>((uint16_t)r.sbits) : 0.f;
+  const float zs = (float)z * sc;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // dword i holds k = 8i .. 8i+7
-    const uint32_t d = r.w[i];
+  for (int i = 0; i < KPT / 8; ++i) {  // dword i holds k = 8i .. 8i+7
+    const uint32_t d = i == 0 ? r.w.x : r.w.y;
     const uint32_t lo4 = d & 0x0F0F0F0Fu, hi4 = (d >> 4) & 0x0F0F0F0Fu;
     float v[8];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      v[2 * b] = fmaf((float)((lo4 >> (8 * b)) & 0xFFu), r.s, -r.zs);      // k = 8i + 2b
-      v[2 * b + 1] = fmaf((float)((hi4 >> (8 * b)) & 0xFFu), r.s, -r.zs);  // k = 8i + 2b + 1
+      v[2 * b] = fmaf((float)((lo4 >> (8 * b)) & 0xFFu), sc, -zs);      // k = 8i + 2b
+      v[2 * b + 1] = fmaf((float)((hi4 >> (8 * b)) & 0xFFu), sc, -zs);  // k = 8i + 2b + 1
     }
     u32x4 h4, l4;
 #pragma unroll
@@ -155,138 +172,270 @@ __device__ __forceinline__ void store_w(const WRegs &r, uint16_t *ws_hi, uint16_
   }
 }
 
-template <int XDT>
-__global__ void __launch_bounds__(NTHREADS, 2)
+// Write 8 consecutive outputs (nv of them in range) to the fp32 copy and / or
+// the output in its dtype; 16-byte stores when `vec` (row pitch and bases
+// allow it) and all 8 are in range.
+__device__ __forceinline__ void store_row8(const float (&v)[8], int nv, bool vec, float *y32,
+                                           void *Y, int ydt, size_t idx) {
+  if (y32) {
+    if (vec && nv == 8) {
+      ((float4_t *)(y32 + idx))[0] = float4_t{v[0], v[1], v[2], v[3]};
+      ((float4_t *)(y32 + idx))[1] = float4_t{v[4], v[5], v[6], v[7]};
+    } else {
+      for (int e = 0; e < nv; ++e) y32[idx + e] = v[e];
+    }
+  }
+  if (!Y) return;
+  if (ydt == SF_F32) {
+    float *d = (float *)Y + idx;
+    if (vec && nv == 8) {
+      ((float4_t *)d)[0] = float4_t{v[0], v[1], v[2], v[3]};
+      ((float4_t *)d)[1] = float4_t{v[4], v[5], v[6], v[7]};
+    } else {
+      for (int e = 0; e < nv; ++e) d[e] = v[e];
+    }
+    return;
+  }
+  uint16_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    b[e] = ydt == SF_BF16 ? sf_f32_to_bf16(v[e]) : sf_bitcast<uint16_t>((f16)v[e]);
+  uint16_t *d = (uint16_t *)Y + idx;
+  if (vec && nv == 8) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = (uint32_t)b[2 * e] | ((uint32_t)b[2 * e + 1] << 16);
+    *(u32x4 *)d = w;
+  } else {
+    for (int e = 0; e < nv; ++e) d[e] = b[e];
+  }
+}
+
+template <int XDT, bool ASYM>
+__global__ void __launch_bounds__(NTHREADS, 1)
 k_q4_gemm(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
           const uint8_t *__restrict__ zt, const void *__restrict__ X, void *__restrict__ Y,
           int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt,
           float *__restrict__ part, int M, int N, int K, int G, int g, int ksplit,
-          int steps_per_split) {
+          int steps_per_split, bool vec) {
   constexpr bool XSPLIT = XDT != SF_BF16;
-  __shared__ __attribute__((aligned(16))) uint16_t xs_hi[BM * LDS_PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t xs_lo[XSPLIT ? BM * LDS_PITCH : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t ws_hi[BN * LDS_PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t ws_lo[BN * LDS_PITCH];
+  constexpr int XB = BM * LDS_PITCH, WB = BN * LDS_PITCH;  // one LDS buffer of each tile
+  constexpr int SMEM_U16 = 2 * XB * (XSPLIT ? 2 : 1) + 4 * WB;
+  constexpr int NWAVES = NTHREADS / 64;
+  static_assert(SMEM_U16 * 2 >= NWAVES * WAVE_M * OUT_PITCH * 4, "output staging must fit");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_U16];
+  uint16_t *const xs_hi = smem;
+  uint16_t *const xs_lo = smem + 2 * XB;  // used only when XSPLIT
+  uint16_t *const ws_hi = smem + 2 * XB * (XSPLIT ? 2 : 1);
+  uint16_t *const ws_lo = ws_hi + 2 * WB;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // wave tile origin in the block tile
+  constexpr int WGN = BN / WAVE_N;  // waves across the tile's columns
+  const int wm = (wave / WGN) * WAVE_M, wn = (wave % WGN) * WAVE_N;  // wave tile origin
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int split = blockIdx.z;
   const int nsteps_total = (K + BK - 1) / BK;
   const int s0 = split * steps_per_split;
   const int s1 = min(s0 + steps_per_split, nsteps_total);
 
-  // staging assignment: row tid/2, 32-element half tid%2
-  const int lrow = tid >> 1, lk = (tid & 1) * 32;
+  // staging assignment: row tid / (BK / KPT), KPT consecutive k
+  const int lrow = tid / (BK / KPT), lk = (tid % (BK / KPT)) * KPT;
 
-  float16_t acc[2][2];
+  float16_t acc[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-  XRegs<XDT> xr;
-  WRegs wr;
-  if (s0 < s1) {
-    load_x<XDT>(xr, X, M, K, m0 + lrow, s0 * BK + lk);
-    load_w(wr, wq, st, zt, N, K, G, g, n0 + lrow, s0 * BK + lk);
-  }
-  for (int step = s0; step < s1; ++step) {
-    __syncthreads();
-    store_x<XDT>(xr, xs_hi, xs_lo, lrow, lk);
-    store_w(wr, ws_hi, ws_lo, lrow, lk);
-    __syncthreads();
-    if (step + 1 < s1) {
-      load_x<XDT>(xr, X, M, K, m0 + lrow, (step + 1) * BK + lk);
-      load_w(wr, wq, st, zt, N, K, G, g, n0 + lrow, (step + 1) * BK + lk);
-    }
+  // Loads past the split's last step re-read that step (in bounds, unused), so
+  // every load is unconditional and stays in flight.
+  auto load = [&](int step, XRegs<XDT> &xr, WRegs &wr) {
+    const int k = min(step, s1 - 1) * BK + lk;
+    load_x<XDT>(xr, X, M, K, m0 + lrow, k);
+    load_w<ASYM>(wr, wq, st, zt, N, K, G, g, n0 + lrow, k);
+  };
+  auto store = [&](int step, const XRegs<XDT> &xr, const WRegs &wr) {
+    const int b = step & 1;
+    store_x<XDT>(xr, xs_hi + b * XB, xs_lo + (XSPLIT ? b * XB : 0), lrow, lk);
+    store_w<ASYM>(wr, ws_hi + b * WB, ws_lo + b * WB, lrow, lk);
+  };
+  auto compute = [&](int step) {
+    const int b = step & 1;
+    const uint16_t *xh = xs_hi + b * XB, *xl = xs_lo + (XSPLIT ? b * XB : 0);
+    const uint16_t *wh = ws_hi + b * WB, *wl = ws_lo + b * WB;
+    const int c = wn + (lane & 31);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       const int kofs = kk + (lane >> 5) * 8;
-      bf16x8_t ah[2], al[2], bh[2], bl[2];
+      bf16x8_t ah[2], al[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int r = wm + i * 32 + (lane & 31);
-        ah[i] = *(const bf16x8_t *)(xs_hi + r * LDS_PITCH + kofs);
-        if constexpr (XSPLIT) al[i] = *(const bf16x8_t *)(xs_lo + r * LDS_PITCH + kofs);
+        ah[i] = *(const bf16x8_t *)(xh + r * LDS_PITCH + kofs);
+        if constexpr (XSPLIT) al[i] = *(const bf16x8_t *)(xl + r * LDS_PITCH + kofs);
       }
+      const bf16x8_t bh = *(const bf16x8_t *)(wh + c * LDS_PITCH + kofs);
+      const bf16x8_t bl = *(const bf16x8_t *)(wl + c * LDS_PITCH + kofs);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int c = wn + j * 32 + (lane & 31);
-        bh[j] = *(const bf16x8_t *)(ws_hi + c * LDS_PITCH + kofs);
-        bl[j] = *(const bf16x8_t *)(ws_lo + c * LDS_PITCH + kofs);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-          if constexpr (XSPLIT) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bl[j], acc[i][j], 0, 0, 0);
-          }
+      for (int i = 0; i < 2; ++i) {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh, acc[i], 0, 0, 0);
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl, acc[i], 0, 0, 0);
+        if constexpr (XSPLIT) {
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bl, acc[i], 0, 0, 0);
         }
+      }
+    }
+  };
+
+  // Pipeline: three register stages of global loads (a step's loads are issued
+  // three steps before it is staged) and two LDS buffers, one barrier per step.
+  // At the top of the loop for step s: LDS buffer s&1 holds step s, xb/wb hold
+  // step s+1, xc/wc step s+2, xa/wa step s+3. Staging is unconditional (past
+  // the end it re-stages the last step into the buffer no one reads again), so
+  // it shares a basic block with the MFMAs and the two can interleave.
+  if (s0 < s1) {
+    XRegs<XDT> xa, xb, xc;
+    WRegs wa, wb, wc;
+    load(s0, xa, wa);
+    load(s0 + 1, xb, wb);
+    load(s0 + 2, xc, wc);
+    store(s0, xa, wa);
+    __syncthreads();
+    load(s0 + 3, xa, wa);
+    for (int s = s0; s < s1; s += 3) {
+      store(s + 1, xb, wb);
+      compute(s);
+      __syncthreads();
+      if (s + 1 >= s1) break;
+      load(s + 4, xb, wb);
+      store(s + 2, xc, wc);
+      compute(s + 1);
+      __syncthreads();
+      if (s + 2 >= s1) break;
+      load(s + 5, xc, wc);
+      store(s + 3, xa, wa);
+      compute(s + 2);
+      __syncthreads();
+      if (s + 3 >= s1) break;
+      load(s + 6, xa, wa);
     }
   }
 
-  // Output: acc[i][j][r] is C[row][col], row = 8*(r/4) + 4*(lane/32) + r%4,
-  // col = lane % 32, within MFMA tile (i, j).
+  // Output. acc[i][r] is C[row][col] with row = 8*(r/4) + 4*(lane/32) + r%4,
+  // col = lane % 32 within MFMA tile i: a lane holds one column, so each wave
+  // stages its WAVE_M x WAVE_N tile in LDS and writes it back as row segments
+  // of 8 values per lane (16-byte stores, whole cache lines per instruction).
+  __syncthreads();  // every wave is done with the operand buffers
+  float *ot = (float *)smem + wave * WAVE_M * OUT_PITCH;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn + j * 32 + (lane & 31);
-      if (col >= N) continue;
-      float bv = 0.f;
-      if (bias && ksplit == 1) {
-        if (bdt == SF_F32) bv = ((const float *)bias)[col];
-        else if (bdt == SF_F16) bv = (float)((const f16 *)bias)[col];
-        else bv = sf_bf16_to_f32(((const uint16_t *)bias)[col]);
-      }
+    for (int r = 0; r < 16; ++r)
+      ot[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * OUT_PITCH + (lane & 31)] = acc[i][r];
+  __syncthreads();
+  constexpr int SEGS = WAVE_N / 8;  // 8-column segments per row
+#pragma unroll 2
+  for (int it = 0; it < WAVE_M * SEGS / 64; ++it) {
+    const int seg = it * 64 + lane;
+    const int rl = seg / SEGS, cl = (seg % SEGS) * 8;
+    const int row = m0 + wm + rl, col = n0 + wn + cl;
+    if (row >= M || col >= N) continue;
+    float v[8];
+    {
+      const float4_t a = *(const float4_t *)(ot + rl * OUT_PITCH + cl);
+      const float4_t c = *(const float4_t *)(ot + rl * OUT_PITCH + cl + 4);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= M) continue;
-        const size_t idx = (size_t)row * N + col;
-        const float v = acc[i][j][r];
-        if (ksplit > 1) {
-          part[(size_t)split * M * N + idx] = v;
-        } else {
-          const float o = v + bv;
-          if (y32) y32[idx] = o;
-          if (Y) {
-            if (ydt == SF_BF16) ((uint16_t *)Y)[idx] = sf_f32_to_bf16(o);
-            else if (ydt == SF_F16) ((f16 *)Y)[idx] = (f16)o;
-            else ((float *)Y)[idx] = o;
-          }
-        }
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = c[e];
       }
     }
+    const int nv = min(8, N - col);
+    const size_t idx = (size_t)row * N + col;
+    if (ksplit > 1) {
+      float *dst = part + (size_t)split * M * N + idx;
+      if (vec && nv == 8) {
+        ((float4_t *)dst)[0] = float4_t{v[0], v[1], v[2], v[3]};
+        ((float4_t *)dst)[1] = float4_t{v[4], v[5], v[6], v[7]};
+      } else {
+        for (int e = 0; e < nv; ++e) dst[e] = v[e];
+      }
+      continue;
+    }
+    if (bias) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int cc = min(col + e, N - 1);
+        if (bdt == SF_F32) v[e] += ((const float *)bias)[cc];
+        else if (bdt == SF_F16) v[e] += (float)((const f16 *)bias)[cc];
+        else v[e] += sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
+      }
+    }
+    store_row8(v, nv, vec, y32, Y, ydt, idx);
+  }
 }
 
+// Sum of the K-split partials in split order (deterministic), plus bias, to
+// the outputs; 8 consecutive elements per thread.
 __global__ void __launch_bounds__(256)
 k_splitk_reduce(const float *__restrict__ part, void *__restrict__ Y, int ydt, float *__restrict__ y32,
-                const void *__restrict__ bias, int bdt, int M, int N, int ksplit) {
+                const void *__restrict__ bias, int bdt, int M, int N, int ksplit, bool vec) {
   const size_t MN = (size_t)M * N;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN;
-       idx += (size_t)gridDim.x * blockDim.x) {
-    float v = 0.f;
-    for (int s = 0; s < ksplit; ++s) v += part[(size_t)s * MN + idx];
-    if (bias) {
-      const int col = (int)(idx % N);
-      if (bdt == SF_F32) v += ((const float *)bias)[col];
-      else if (bdt == SF_F16) v += (float)((const f16 *)bias)[col];
-      else v += sf_bf16_to_f32(((const uint16_t *)bias)[col]);
+  const size_t n8 = (MN + 7) / 8;
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8;
+       t += (size_t)gridDim.x * blockDim.x) {
+    const size_t idx = t * 8;
+    const int row = (int)(idx / N), col = (int)(idx - (size_t)row * N);
+    float v[8];
+    int nv = 8;
+    if (vec) {  // N % 8 == 0: the 8 elements are in one row
+      float4_t a = {0.f, 0.f, 0.f, 0.f}, c = a;
+      for (int s = 0; s < ksplit; ++s) {
+        a += ((const float4_t *)(part + (size_t)s * MN + idx))[0];
+        c += ((const float4_t *)(part + (size_t)s * MN + idx))[1];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = c[e];
+      }
+    } else {
+      nv = (int)min((size_t)8, MN - idx);
+      for (int e = 0; e < 8; ++e) {
+        v[e] = 0.f;
+        if (e < nv)
+          for (int s = 0; s < ksplit; ++s) v[e] += part[(size_t)s * MN + idx + e];
+      }
     }
-    if (y32) y32[idx] = v;
-    if (Y) {
-      if (ydt == SF_BF16) ((uint16_t *)Y)[idx] = sf_f32_to_bf16(v);
-      else if (ydt == SF_F16) ((f16 *)Y)[idx] = (f16)v;
-      else ((float *)Y)[idx] = v;
+    if (vec) {
+      if (bias)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int cc = col + e;
+          if (bdt == SF_F32) v[e] += ((const float *)bias)[cc];
+          else if (bdt == SF_F16) v[e] += (float)((const f16 *)bias)[cc];
+          else v[e] += sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
+        }
+      store_row8(v, 8, true, y32, Y, ydt, idx);
+    } else {
+      for (int e = 0; e < nv; ++e) {
+        float o = v[e];
+        const size_t id = idx + e;
+        if (bias) {
+          const int cc = (int)(id % N);
+          if (bdt == SF_F32) o += ((const float *)bias)[cc];
+          else if (bdt == SF_F16) o += (float)((const f16 *)bias)[cc];
+          else o += sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
+        }
+        if (y32) y32[id] = o;
+        if (Y) {
+          if (ydt == SF_BF16) ((uint16_t *)Y)[id] = sf_f32_to_bf16(o);
+          else if (ydt == SF_F16) ((f16 *)Y)[id] = (f16)o;
+          else ((float *)Y)[id] = o;
+        }
+      }
     }
   }
 }
@@ -344,18 +493,28 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, ksplit);
   float *part = (float *)workspace;
-#define SF_GEMM_LAUNCH(XD)                                                                       \
-  k_q4_gemm<XD><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, part, \
-                                          M, N, K, L.G, group_size, ksplit, steps_per_split)
-  if (x_dtype == SF_BF16) SF_GEMM_LAUNCH(SF_BF16);
-  else if (x_dtype == SF_F16) SF_GEMM_LAUNCH(SF_F16);
-  else SF_GEMM_LAUNCH(SF_F32);
+  // 16-byte output stores need rows of whole 16-byte multiples and aligned bases
+  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)y_f32 & 15) == 0 &&
+                   ((uintptr_t)part & 15) == 0;
+#define SF_GEMM_LAUNCH(XD, AS)                                                                 \
+  k_q4_gemm<XD, AS><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, \
+                                              part, M, N, K, L.G, group_size, ksplit,            \
+                                              steps_per_split, vec)
+#define SF_GEMM_X(AS)                                  \
+  do {                                                 \
+    if (x_dtype == SF_BF16) SF_GEMM_LAUNCH(SF_BF16, AS); \
+    else if (x_dtype == SF_F16) SF_GEMM_LAUNCH(SF_F16, AS); \
+    else SF_GEMM_LAUNCH(SF_F32, AS);                   \
+  } while (0)
+  if (has_zeros) SF_GEMM_X(true);
+  else SF_GEMM_X(false);
+#undef SF_GEMM_X
 #undef SF_GEMM_LAUNCH
   int rc = sf_check_launch("sf_q4_gemm");
   if (rc || ksplit == 1) return rc;
-  const size_t MN = (size_t)M * N;
-  unsigned rg = (unsigned)((MN + 255) / 256);
+  const size_t n8 = ((size_t)M * N + 7) / 8;
+  unsigned rg = (unsigned)((n8 + 255) / 256);
   if (rg > 65535u * 16u) rg = 65535u * 16u;
-  k_splitk_reduce<<<rg, 256, 0, s>>>(part, y, y_dtype, y_f32, bias, bias_dtype, M, N, ksplit);
+  k_splitk_reduce<<<rg, 256, 0, s>>>(part, y, y_dtype, y_f32, bias, bias_dtype, M, N, ksplit, vec);
   return sf_check_launch("sf_q4_gemm(reduce)");
 }
