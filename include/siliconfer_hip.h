@@ -129,6 +129,71 @@ int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const
                         int KVH, int T, int T_cap, int D, float scale, int n_splits,
                         void *stream);
 
+/* The same attention with its length in device memory: T = *T_dev + T_add
+ * (for decode steps replayed from a HIP graph, where the length grows by one
+ * token per replay). n_splits (<= 0: sf_attn_default_splits at T_max) and the
+ * workspace are fixed for T <= T_max. Same reference interface as above. */
+int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                            const void *k_scales, const int8_t *v_codes, const void *v_scales,
+                            int scale_dtype, void *out, int out_dtype, void *workspace,
+                            size_t workspace_bytes, int B, int H, int KVH, const int *T_dev,
+                            int T_add, int T_max, int T_cap, int D, float scale, int n_splits,
+                            void *stream);
+
+/* Causal prefill attention over a batch-1 int8 cache: query row i of q
+ * [T_q][H][D] attends to the first T0 + i + 1 cached tokens (the prompt's own
+ * keys already appended). Replaces the reference's prompt path, which
+ * dequantizes the whole cache and runs SDPA with an additive causal mask
+ * (/root/reference/siliconfer/model/layers.py:108-126). Output [T_q][H][D]. */
+int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const void *k_scales,
+                         const int8_t *v_codes, const void *v_scales, int scale_dtype, void *out,
+                         int out_dtype, int T_q, int H, int KVH, int T0, int T_cap, int D,
+                         float scale, void *stream);
+
+/* ---- decoder step operations (model runner) -------------------------------
+ * The per-token work of the reference's TransformerBlock / LlamaModel around
+ * the projections (/root/reference/siliconfer/model/layers.py:14-163,
+ * model/llama.py:38-83). Row-major fp32 residual stream. */
+
+/* Embedding gather: out[r][:] = table[ids[r]][:] (nn.Embedding, llama.py:55).
+ * ids int32 on the device (out-of-range ids are clamped). */
+int sf_embed(const int32_t *ids, const void *table, int table_dtype, float *out, int rows, int H,
+             int V, void *stream);
+
+/* RMSNorm (layers.py:14-21, mx.fast.rms_norm): if delta, x += delta in place
+ * (the residual add of layers.py:160-162); then
+ * out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w. */
+int sf_rmsnorm(float *x, const float *delta, const void *w, int w_dtype, void *out, int out_dtype,
+               int rows, int H, float eps, void *stream);
+
+/* RoPE (layers.py:58-66, rotate-half) of the q and k heads of the fused q|k|v
+ * projection rows qkv [rows][(H + 2 KVH) * D] at positions pos0 + r, then the
+ * int8 quantize-append of k and v into a batch-1 cache [KVH][T_cap][D] with the
+ * rule of sf_kv_quant_append (kv_cache.py:49-63, 90-105). cos_t / sin_t are
+ * fp32 [max_pos][D/2] tables of position * freq (layers.py:24-33). pos0 is
+ * *pos_dev when pos_dev is not NULL (device-side decode position), else
+ * pos_host. Rotated q goes to q_out [rows][H][D]. */
+int sf_rope_kv_append(const float *qkv, const float *cos_t, const float *sin_t, int max_pos,
+                      void *q_out, int q_dtype, int8_t *k_codes, void *k_scales, int8_t *v_codes,
+                      void *v_scales, int scale_dtype, int rows, int H, int KVH, int D, int T_cap,
+                      const int *pos_dev, int pos_host, void *stream);
+
+/* SwiGLU activation (layers.py:143-144): out[r][i] = silu(gu[r][i]) *
+ * gu[r][I + i] for the fused gate|up projection rows gu [rows][2 I]. */
+int sf_silu_mul(const float *gu, void *out, int out_dtype, int rows, int I, void *stream);
+
+/* Tied-embedding logits and greedy token (llama.py:77-79 `as_linear`,
+ * generate.py:45-46 argmax): logits[v] = sum_k W[v][k] x[k] for bf16 W [V][H],
+ * written as fp32 when logits is not NULL; *token_out = argmax (lowest index
+ * on ties). When pos_inc is not NULL: hist[*pos_inc] = token (if hist is not
+ * NULL), then *pos_inc += 1 — the device-side decode position. The workspace
+ * (sf_lm_head_workspace_bytes, 256-byte aligned) must be zero-filled before
+ * its first use; each call leaves it so. */
+size_t sf_lm_head_workspace_bytes(int V);
+int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, float *logits, int V, int H,
+                      int32_t *token_out, int *pos_inc, int32_t *hist, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

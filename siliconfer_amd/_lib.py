@@ -44,6 +44,19 @@ _SIGS = {
     "sf_attn_decode_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                    _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f,
                                    _c_i, _c_p]),
+    "sf_attn_decode_i8kv_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
+                                       _c_p, _c_sz, _c_i, _c_i, _c_i, _c_p, _c_i, _c_i, _c_i,
+                                       _c_i, _c_f, _c_i, _c_p]),
+    "sf_attn_prefill_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
+                                    _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_p]),
+    "sf_embed": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p]),
+    "sf_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_f, _c_p]),
+    "sf_rope_kv_append": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p,
+                                 _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_i, _c_p]),
+    "sf_silu_mul": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_i, _c_p]),
+    "sf_lm_head_workspace_bytes": (_c_sz, [_c_i]),
+    "sf_lm_head_argmax": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p,
+                                 _c_sz, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -184,8 +184,8 @@ __global__ void __launch_bounds__(kAttnThreads)
 k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
               const void *__restrict__ ks, const int8_t *__restrict__ vc,
               const void *__restrict__ vs, float *part_acc, float *part_ml, unsigned *counters,
-              void *__restrict__ out, int odt, int H, int KVH, int T, int T_cap, int D,
-              float qscale, int n_splits, int tile, int oct_log2) {
+              void *__restrict__ out, int odt, int H, int KVH, int T, const int *__restrict__ T_dev,
+              int causal, int T_cap, int D, float qscale, int n_splits, int oct_log2) {
   constexpr int NT = kAttnThreads, NW = kAttnWaves, U = kAttnBatch;
   __shared__ __attribute__((aligned(16))) float smem[attn_smem_floats<HB>()];
   __shared__ int s_last;
@@ -208,8 +208,15 @@ k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
   const int d0 = oct * 8;
   const bool dact = d0 < D;
   const int dq = dact ? d0 : 0;
-  const int t0 = split * tile, t1 = min(t0 + tile, T);
-  const size_t base = ((size_t)b * KVH + kvh) * (size_t)T_cap;
+  // Length: the host's T, or a device length plus T (decode steps replayed
+  // from a graph), or for a causal prefill T tokens before query row b plus
+  // the row itself; the cache then has batch 1.
+  int Tv = T_dev ? *T_dev + T : T;
+  if (causal) Tv = T + b + 1;
+  Tv = max(0, min(Tv, T_cap));
+  const int tile = (Tv + n_splits - 1) / n_splits;
+  const int t0 = split * tile, t1 = min(t0 + tile, Tv);
+  const size_t base = ((size_t)(causal ? 0 : b) * KVH + kvh) * (size_t)T_cap;
   const size_t bh0 = (size_t)b * H + (size_t)kvh * G + (size_t)hblk * HB;
 
   float qr[HB][8];
@@ -605,45 +612,45 @@ static int attn_heads_per_block(int G) {
   return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 6 ? 6 : G <= 7 ? 7 : 8;
 }
 
-extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
-                                   const void *k_scales, const int8_t *v_codes,
-                                   const void *v_scales, int scale_dtype, void *out, int out_dtype,
-                                   void *workspace, size_t workspace_bytes, int B, int H, int KVH,
-                                   int T, int T_cap, int D, float scale, int n_splits,
-                                   void *stream) {
-  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
-             "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
+// Shared checks and launch. T_dev: device length (plus T); causal: prefill
+// rows, query row b sees T + b + 1 tokens of a batch-1 cache.
+static int attn_launch(const char *what, const void *q, int q_dtype, const int8_t *k_codes,
+                       const void *k_scales, const int8_t *v_codes, const void *v_scales,
+                       int scale_dtype, void *out, int out_dtype, void *workspace,
+                       size_t workspace_bytes, int B, int H, int KVH, int T, const int *T_dev,
+                       int causal, int T_cap, int D, float scale, int n_splits, void *stream) {
   SF_REQUIRE(H % KVH == 0, SF_EINVAL, "n_heads=%d not a multiple of n_kv_heads=%d", H, KVH);
   SF_REQUIRE(D <= kMaxD, SF_EINVAL, "head_dim=%d exceeds kernel's compile-time max 256", D);
   SF_REQUIRE(D % 8 == 0, SF_EUNSUPPORTED, "head_dim=%d: need a multiple of 8", D);
-  SF_REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out && workspace, SF_EINVAL,
+  SF_REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out, SF_EINVAL,
              "null pointer argument");
   SF_REQUIRE(q_dtype >= SF_F32 && q_dtype <= SF_BF16 && out_dtype >= SF_F32 && out_dtype <= SF_BF16,
              SF_EINVAL, "bad q/out dtype");
   SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
              scale_dtype);
-  SF_REQUIRE(((uintptr_t)workspace & 255) == 0, SF_EINVAL, "workspace must be 256-byte aligned");
   SF_REQUIRE((((uintptr_t)k_codes | (uintptr_t)v_codes) & 7) == 0, SF_EINVAL,
              "KV code buffers must be 8-byte aligned");
   SF_REQUIRE(((uintptr_t)q & 15) == 0, SF_EINVAL, "q must be 16-byte aligned");
-  if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T);
-  // the reference's tiling: n_tiles = max(1, min(n_tiles, T)); tile = ceil(T / n_tiles)
-  n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
   if (n_splits > kMaxSplits) n_splits = kMaxSplits;
   if (n_splits < 1) n_splits = 1;
-  const int tile = T > 0 ? (T + n_splits - 1) / n_splits : 0;
-  const size_t need = sf_attn_workspace_bytes(B, H, D, n_splits);
-  SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "attention workspace too small: %zu < %zu",
-             workspace_bytes, need);
-  size_t acc_off, ml_off;
-  attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
-  float *part_acc = (float *)((char *)workspace + acc_off);
-  float *part_ml = (float *)((char *)workspace + ml_off);
-  unsigned *counters = (unsigned *)workspace;
+  size_t acc_off = 0, ml_off = 0;
+  float *part_acc = nullptr, *part_ml = nullptr;
+  unsigned *counters = nullptr;
+  if (n_splits > 1) {
+    SF_REQUIRE(workspace, SF_EINVAL, "null workspace");
+    SF_REQUIRE(((uintptr_t)workspace & 255) == 0, SF_EINVAL, "workspace must be 256-byte aligned");
+    const size_t need = sf_attn_workspace_bytes(B, H, D, n_splits);
+    SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "attention workspace too small: %zu < %zu",
+               workspace_bytes, need);
+    attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
+    part_acc = (float *)((char *)workspace + acc_off);
+    part_ml = (float *)((char *)workspace + ml_off);
+    counters = (unsigned *)workspace;
+  }
   const int G = H / KVH;
   const int HB = attn_heads_per_block(G);
   const int n_hblk = (G + HB - 1) / HB;
-  SF_REQUIRE(B * KVH * n_hblk <= kMaxCounters, SF_EUNSUPPORTED,
+  SF_REQUIRE(n_splits == 1 || B * KVH * n_hblk <= kMaxCounters, SF_EUNSUPPORTED,
              "attention batch too large for one call (B * n_kv_heads * head blocks = %d > %d)",
              B * KVH * n_hblk, kMaxCounters);
   const int oct_log2 = pow2_log2_at_least(D / 8);
@@ -653,7 +660,7 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
 #define SF_ATTN_LAUNCH(QD, SD, HBV)                                                            \
   k_attn_decode<QD, SD, HBV><<<grid, kAttnThreads, 0, st>>>(                                   \
       q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H, \
-      KVH, T, T_cap, D, qscale, n_splits, tile, oct_log2)
+      KVH, T, T_dev, causal, T_cap, D, qscale, n_splits, oct_log2)
 #define SF_ATTN_HB(QD, SD)                       \
   do {                                           \
     if (HB == 1) SF_ATTN_LAUNCH(QD, SD, 1);      \
@@ -674,5 +681,51 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
   }
 #undef SF_ATTN_HB
 #undef SF_ATTN_LAUNCH
-  return sf_check_launch("sf_attn_decode_i8kv");
+  return sf_check_launch(what);
+}
+
+extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
+                                   const void *k_scales, const int8_t *v_codes,
+                                   const void *v_scales, int scale_dtype, void *out, int out_dtype,
+                                   void *workspace, size_t workspace_bytes, int B, int H, int KVH,
+                                   int T, int T_cap, int D, float scale, int n_splits,
+                                   void *stream) {
+  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
+             "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
+  if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T);
+  // the reference's tiling: n_tiles = max(1, min(n_tiles, T)); tile = ceil(T / n_tiles)
+  n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
+  if (n_splits > kMaxSplits) n_splits = kMaxSplits;
+  return attn_launch("sf_attn_decode_i8kv", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
+                     scale_dtype, out, out_dtype, workspace, workspace_bytes, B, H, KVH, T,
+                     nullptr, 0, T_cap, D, scale, n_splits, stream);
+}
+
+extern "C" int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                                       const void *k_scales, const int8_t *v_codes,
+                                       const void *v_scales, int scale_dtype, void *out,
+                                       int out_dtype, void *workspace, size_t workspace_bytes, int B,
+                                       int H, int KVH, const int *T_dev, int T_add, int T_max,
+                                       int T_cap, int D, float scale, int n_splits, void *stream) {
+  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T_max >= 0 && T_max <= T_cap, SF_EINVAL,
+             "invalid attention shape B=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", B, H, KVH, T_max,
+             T_cap, D);
+  SF_REQUIRE(T_dev, SF_EINVAL, "null pointer argument");
+  if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T_max);
+  return attn_launch("sf_attn_decode_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
+                     scale_dtype, out, out_dtype, workspace, workspace_bytes, B, H, KVH, T_add,
+                     T_dev, 0, T_cap, D, scale, n_splits, stream);
+}
+
+extern "C" int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
+                                    const void *k_scales, const int8_t *v_codes,
+                                    const void *v_scales, int scale_dtype, void *out,
+                                    int out_dtype, int T_q, int H, int KVH, int T0, int T_cap,
+                                    int D, float scale, void *stream) {
+  SF_REQUIRE(T_q > 0 && H > 0 && KVH > 0 && D > 0 && T0 >= 0 && T0 + T_q <= T_cap, SF_EINVAL,
+             "invalid prefill attention shape T_q=%d H=%d KVH=%d T0=%d T_cap=%d D=%d", T_q, H, KVH,
+             T0, T_cap, D);
+  return attn_launch("sf_attn_prefill_i8kv", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
+                     scale_dtype, out, out_dtype, nullptr, 0, T_q, H, KVH, T0, nullptr, 1, T_cap, D,
+                     scale, 1, stream);
 }

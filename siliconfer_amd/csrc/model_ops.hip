@@ -1,0 +1,456 @@
+// model_ops.hip — the small per-token operations of the decoder around the
+// int4 projections and the int8-KV attention (gfx950), for the model runner
+// that restates the reference's LlamaModel / generate
+// (/root/reference/siliconfer/model/layers.py:14-163, model/llama.py:38-83,
+// engine/generate.py:117-180):
+//
+//   sf_embed            token ids -> fp32 residual rows (embedding gather)
+//   sf_rmsnorm          optional residual add, then x * rsqrt(mean(x^2) + eps) * w
+//   sf_rope_kv_append   rotate-half RoPE of q and k (host-computed fp32 cos /
+//                       sin tables) and the int8 quantize-append of k and v
+//   sf_silu_mul         silu(gate) * up
+//   sf_lm_head_argmax   dense bf16 logits (the tied embedding) and the greedy
+//                       token, with an optional device position increment
+//
+// Positions and the greedy token can live in device memory, so one decode
+// step is a fixed sequence of launches that a HIP graph replays token after
+// token with no host round trip.
+#include <math.h>
+
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Sum over the block (blockDim.x a multiple of 64, at most 1024); every
+// thread gets the result. `red` holds one float per wave.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < nw; ++w) t += red[w];
+  return t;
+}
+
+__device__ __forceinline__ void store_as(void *p, int dt, size_t i, float v) {
+  if (dt == SF_F32) ((float *)p)[i] = v;
+  else if (dt == SF_F16) ((f16 *)p)[i] = (f16)v;
+  else ((uint16_t *)p)[i] = sf_f32_to_bf16(v);
+}
+
+__device__ __forceinline__ float load_as(const void *p, int dt, size_t i) {
+  if (dt == SF_F32) return ((const float *)p)[i];
+  if (dt == SF_F16) return (float)((const f16 *)p)[i];
+  return sf_bf16_to_f32(((const uint16_t *)p)[i]);
+}
+
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads)
+k_embed(const int32_t *__restrict__ ids, const void *__restrict__ table, int tdt,
+        float *__restrict__ out, int H, int V) {
+  const int r = blockIdx.x;
+  int id = ids[r];
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);  // ids are validated on the host
+  for (int h = threadIdx.x; h < H; h += blockDim.x)
+    out[(size_t)r * H + h] = load_as(table, tdt, (size_t)id * H + h);
+}
+
+// ---------------------------------------------------------------------------
+// One block per row. mx.fast.rms_norm semantics: fp32 mean of squares,
+// x * rsqrt(mean + eps) * w.
+__global__ void __launch_bounds__(kThreads)
+k_rmsnorm(float *__restrict__ x, const float *__restrict__ delta, const void *__restrict__ w,
+          int wdt, void *__restrict__ out, int odt, int H, float eps) {
+  __shared__ float red[kThreads / 64];
+  const size_t r0 = (size_t)blockIdx.x * H;
+  float ss = 0.f;
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    float v = x[r0 + h];
+    if (delta) {
+      v += delta[r0 + h];
+      x[r0 + h] = v;
+    }
+    ss = fmaf(v, v, ss);
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / (float)H + eps);
+  for (int h = threadIdx.x; h < H; h += blockDim.x)
+    store_as(out, odt, r0 + h, x[r0 + h] * inv * load_as(w, wdt, h));
+}
+
+// ---------------------------------------------------------------------------
+// One wave per (row, head) of the fused q|k|v projection output
+// qkv [rows][(H + 2 KVH) * D]. Rotate-half RoPE (layers.py:58-66):
+// out[d] = x[d] cos - x[d + D/2] sin, out[d + D/2] = x[d + D/2] cos + x[d] sin,
+// with cos / sin of (position * freq_d) from the host-made fp32 tables. q goes
+// to q_out; rotated k and raw v are quantized per (head, token) exactly as
+// sf_kv_quant_append does (s = max|x| / 127, 1 if 0; code = clip(rint(x / s)))
+// into the cache at position pos0 + row (batch 1).
+template <int QDT, int SDT>
+__global__ void __launch_bounds__(64)
+k_rope_kv_append(const float *__restrict__ qkv, const float *__restrict__ cos_t,
+                 const float *__restrict__ sin_t, int max_pos, void *__restrict__ q_out,
+                 int8_t *__restrict__ k_codes, void *__restrict__ k_scales,
+                 int8_t *__restrict__ v_codes, void *__restrict__ v_scales, int H, int KVH, int D,
+                 int T_cap, const int *__restrict__ pos_dev, int pos_host) {
+  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+  const int pos = (pos_dev ? *pos_dev : pos_host) + row;
+  const int half = D >> 1;
+  const int width = (H + 2 * KVH) * D;
+  const float *x = qkv + (size_t)row * width + (size_t)head * D;
+  const bool is_q = head < H, is_k = !is_q && head < H + KVH;
+  if (pos < 0 || pos >= T_cap || pos >= max_pos) return;  // the host keeps positions in range
+  // each lane owns the dimension pairs (d, d + D/2) for d = lane, lane + 64, ...
+  constexpr int MAXP = 2;  // D <= 256
+  float lo[MAXP], hi[MAXP];
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) {
+    const int d = lane + 64 * j;
+    lo[j] = hi[j] = 0.f;
+    if (d < half) {
+      const float a = x[d], b = x[d + half];
+      if (is_q || is_k) {
+        // separately rounded products, as x * cos + rotate(x) * sin in fp32
+#pragma clang fp contract(off)
+        const float c = cos_t[(size_t)pos * half + d], s = sin_t[(size_t)pos * half + d];
+        lo[j] = a * c - b * s;
+        hi[j] = b * c + a * s;
+      } else {
+        lo[j] = a;
+        hi[j] = b;
+      }
+    }
+  }
+  if (is_q) {
+#pragma unroll
+    for (int j = 0; j < MAXP; ++j) {
+      const int d = lane + 64 * j;
+      if (d < half) {
+        const size_t o = ((size_t)row * H + head) * D + d;
+        sf_store_from_f32<QDT>(q_out, o, lo[j]);
+        sf_store_from_f32<QDT>(q_out, o + half, hi[j]);
+      }
+    }
+    return;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) amax = fmaxf(amax, fmaxf(fabsf(lo[j]), fabsf(hi[j])));
+  amax = wave_max(amax);
+  const float s = amax == 0.f ? 1.f : amax / 127.f;
+  const int kvh = is_k ? head - H : head - H - KVH;
+  const size_t crow = (size_t)kvh * T_cap + pos;
+  int8_t *codes = (is_k ? k_codes : v_codes) + crow * D;
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) {
+    const int d = lane + 64 * j;
+    if (d < half) {
+      codes[d] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(lo[j] / s), -128.f), 127.f);
+      codes[d + half] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(hi[j] / s), -128.f), 127.f);
+    }
+  }
+  if (lane == 0) sf_store_from_f32<SDT>(is_k ? k_scales : v_scales, crow, s);
+}
+
+// ---------------------------------------------------------------------------
+// out[r][i] = silu(gu[r][i]) * gu[r][I + i], silu(g) = g / (1 + exp(-g)).
+__global__ void __launch_bounds__(kThreads)
+k_silu_mul(const float *__restrict__ gu, void *__restrict__ out, int odt, int I, long long n) {
+  for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+       t += (long long)gridDim.x * blockDim.x) {
+    const long long r = t / I, i = t - r * I;
+    const float g = gu[r * 2 * I + i], u = gu[r * 2 * I + I + i];
+    store_as(out, odt, (size_t)t, g / (1.f + expf(-g)) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// logits[v] = sum_k W[v][k] x[k], W bf16 [V][H] (the tied embedding table), x
+// staged in LDS as fp32. A wave takes rows w, w + n_waves, ...: its lanes load
+// the row in 16-byte chunks (8 bf16), four rows in flight, and a DPP tree
+// sums each row. Every wave keeps its best (value, index) — greedy argmax,
+// lowest index on ties like mx.argmax — the block folds them, writes its
+// partial with agent-scope atomic stores, and the last block to finish
+// (counter) folds all partials, writes the token, resets the counter and
+// increments the device position if asked.
+constexpr int kHeadBlocks = 1024;
+constexpr int kHeadMaxH = 8192;
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int XDT>
+__global__ void __launch_bounds__(kThreads)
+k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
+                 float *__restrict__ logits, int V, int H, int32_t *__restrict__ token_out,
+                 int *__restrict__ pos_inc, int32_t *__restrict__ hist, float *part_val,
+                 int *part_idx, unsigned *counter) {
+  __shared__ __attribute__((aligned(16))) float xs[kHeadMaxH];
+  __shared__ float bv_s[kThreads / 64];
+  __shared__ int bi_s[kThreads / 64];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int h = tid; h < H; h += kThreads) xs[h] = sf_load_as_f32<XDT>(x, h);
+  __syncthreads();
+  const int nch = H >> 3;  // 16-byte chunks per row
+  const int n_waves = gridDim.x * (kThreads / 64);
+  const int gw = blockIdx.x * (kThreads / 64) + wave;
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  constexpr int RU = 4;   // rows in flight per wave
+  constexpr int CPL = 2;  // chunks per lane (H <= 1024 in one pass)
+  for (int r0 = gw; r0 < V; r0 += RU * n_waves) {
+    u32x4 c[RU][CPL];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int row = min(r0 + u * n_waves, V - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int ch = min(lane + 64 * j, nch - 1);
+        c[u][j] = *(const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8);
+      }
+    }
+    // rows longer than CPL * 64 chunks: the rest, one pass at a time
+    float acc[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int ch = lane + 64 * j;
+        if (ch < nch) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t p = c[u][j][e];
+            a = fmaf(sf_bitcast<float>(p << 16), xs[ch * 8 + 2 * e], a);
+            a = fmaf(sf_bitcast<float>(p & 0xffff0000u), xs[ch * 8 + 2 * e + 1], a);
+          }
+        }
+      }
+      const int row = r0 + u * n_waves;
+      for (int ch = lane + 64 * CPL; ch < nch; ch += 64) {
+        const u32x4 q = *(const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a = fmaf(sf_bitcast<float>(q[e] << 16), xs[ch * 8 + 2 * e], a);
+          a = fmaf(sf_bitcast<float>(q[e] & 0xffff0000u), xs[ch * 8 + 2 * e + 1], a);
+        }
+      }
+      acc[u] = a;
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const float a = wave_sum(acc[u]);
+      const int row = r0 + u * n_waves;
+      if (row < V) {
+        if (lane == 0 && logits) logits[row] = a;
+        if (better(a, row, best, best_i)) {
+          best = a;
+          best_i = row;
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+    bv_s[wave] = best;
+    bi_s[wave] = best_i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float b = bv_s[0];
+    int bi = bi_s[0];
+    for (int k = 1; k < kThreads / 64; ++k)
+      if (better(bv_s[k], bi_s[k], b, bi)) {
+        b = bv_s[k];
+        bi = bi_s[k];
+      }
+    __hip_atomic_store((uint32_t *)(part_val + blockIdx.x), sf_bitcast<uint32_t>(b),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(part_idx + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the partial is stored before the count
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  float b = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int k = tid; k < (int)gridDim.x; k += kThreads) {
+    const float v = sf_bitcast<float>(__hip_atomic_load((const uint32_t *)(part_val + k),
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int i = __hip_atomic_load(part_idx + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (better(v, i, b, bi)) {
+      b = v;
+      bi = i;
+    }
+  }
+  // fold (value, index) over the block
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(b, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (better(ov, oi, b, bi)) {
+      b = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    bv_s[wave] = b;
+    bi_s[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float fb = bv_s[0];
+    int fi = bi_s[0];
+    for (int k = 1; k < kThreads / 64; ++k)
+      if (better(bv_s[k], bi_s[k], fb, fi)) {
+        fb = bv_s[k];
+        fi = bi_s[k];
+      }
+    const int tok = fi == 0x7fffffff ? 0 : fi;
+    token_out[0] = tok;
+    if (pos_inc) {
+      const int p = pos_inc[0];
+      if (hist) hist[p] = tok;
+      pos_inc[0] = p + 1;
+    }
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int sf_embed(const int32_t *ids, const void *table, int table_dtype, float *out,
+                        int rows, int H, int V, void *stream) {
+  SF_REQUIRE(rows > 0 && H > 0 && V > 0, SF_EINVAL, "invalid embedding shape rows=%d H=%d V=%d",
+             rows, H, V);
+  SF_REQUIRE(ids && table && out, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(table_dtype >= SF_F32 && table_dtype <= SF_BF16, SF_EINVAL, "bad table dtype %d",
+             table_dtype);
+  k_embed<<<rows, kThreads, 0, (hipStream_t)stream>>>(ids, table, table_dtype, out, H, V);
+  return sf_check_launch("sf_embed");
+}
+
+extern "C" int sf_rmsnorm(float *x, const float *delta, const void *w, int w_dtype, void *out,
+                          int out_dtype, int rows, int H, float eps, void *stream) {
+  SF_REQUIRE(rows > 0 && H > 0, SF_EINVAL, "invalid rmsnorm shape rows=%d H=%d", rows, H);
+  SF_REQUIRE(x && w && out, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(w_dtype >= SF_F32 && w_dtype <= SF_BF16 && out_dtype >= SF_F32 && out_dtype <= SF_BF16,
+             SF_EINVAL, "bad rmsnorm dtype");
+  k_rmsnorm<<<rows, kThreads, 0, (hipStream_t)stream>>>(x, delta, w, w_dtype, out, out_dtype, H,
+                                                         eps);
+  return sf_check_launch("sf_rmsnorm");
+}
+
+extern "C" int sf_rope_kv_append(const float *qkv, const float *cos_t, const float *sin_t,
+                                 int max_pos, void *q_out, int q_dtype, int8_t *k_codes,
+                                 void *k_scales, int8_t *v_codes, void *v_scales, int scale_dtype,
+                                 int rows, int H, int KVH, int D, int T_cap, const int *pos_dev,
+                                 int pos_host, void *stream) {
+  SF_REQUIRE(rows > 0 && H > 0 && KVH > 0 && D > 0 && T_cap > 0 && max_pos > 0, SF_EINVAL,
+             "invalid rope/append shape rows=%d H=%d KVH=%d D=%d T_cap=%d", rows, H, KVH, D,
+             T_cap);
+  SF_REQUIRE(D % 2 == 0 && D <= 256, SF_EUNSUPPORTED, "head_dim=%d: need an even D <= 256", D);
+  SF_REQUIRE(qkv && cos_t && sin_t && q_out && k_codes && k_scales && v_codes && v_scales,
+             SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(q_dtype >= SF_F32 && q_dtype <= SF_BF16, SF_EINVAL, "bad q dtype %d", q_dtype);
+  SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
+             scale_dtype);
+  if (!pos_dev)
+    SF_REQUIRE(pos_host >= 0 && pos_host + rows <= T_cap && pos_host + rows <= max_pos, SF_EINVAL,
+               "positions %d..%d exceed the cache capacity %d or the RoPE table %d", pos_host,
+               pos_host + rows - 1, T_cap, max_pos);
+  dim3 grid(rows, H + 2 * KVH);
+  hipStream_t st = (hipStream_t)stream;
+#define SF_ROPE_LAUNCH(QD, SD)                                                                    \
+  k_rope_kv_append<QD, SD><<<grid, 64, 0, st>>>(qkv, cos_t, sin_t, max_pos, q_out, k_codes,        \
+                                                 k_scales, v_codes, v_scales, H, KVH, D, T_cap,    \
+                                                 pos_dev, pos_host)
+  if (scale_dtype == SF_F16) {
+    if (q_dtype == SF_F32) SF_ROPE_LAUNCH(SF_F32, SF_F16);
+    else if (q_dtype == SF_F16) SF_ROPE_LAUNCH(SF_F16, SF_F16);
+    else SF_ROPE_LAUNCH(SF_BF16, SF_F16);
+  } else {
+    if (q_dtype == SF_F32) SF_ROPE_LAUNCH(SF_F32, SF_F32);
+    else if (q_dtype == SF_F16) SF_ROPE_LAUNCH(SF_F16, SF_F32);
+    else SF_ROPE_LAUNCH(SF_BF16, SF_F32);
+  }
+#undef SF_ROPE_LAUNCH
+  return sf_check_launch("sf_rope_kv_append");
+}
+
+extern "C" int sf_silu_mul(const float *gu, void *out, int out_dtype, int rows, int I,
+                           void *stream) {
+  SF_REQUIRE(rows > 0 && I > 0, SF_EINVAL, "invalid silu_mul shape rows=%d I=%d", rows, I);
+  SF_REQUIRE(gu && out, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(out_dtype >= SF_F32 && out_dtype <= SF_BF16, SF_EINVAL, "bad out dtype %d", out_dtype);
+  const long long n = (long long)rows * I;
+  long long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;
+  k_silu_mul<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(gu, out, out_dtype, I, n);
+  return sf_check_launch("sf_silu_mul");
+}
+
+extern "C" size_t sf_lm_head_workspace_bytes(int V) {
+  (void)V;
+  // counter (256 B slot), then kHeadBlocks (value, index) partials
+  return 256 + (size_t)kHeadBlocks * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, float *logits, int V,
+                                 int H, int32_t *token_out, int *pos_inc, int32_t *hist,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  SF_REQUIRE(V > 0 && H > 0, SF_EINVAL, "invalid lm_head shape V=%d H=%d", V, H);
+  SF_REQUIRE(H % 8 == 0 && H <= kHeadMaxH, SF_EUNSUPPORTED,
+             "hidden=%d: need a multiple of 8 up to %d", H, kHeadMaxH);
+  SF_REQUIRE(w && x && token_out && workspace, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(!hist || pos_inc, SF_EINVAL, "a token history needs the device position");
+  SF_REQUIRE(x_dtype >= SF_F32 && x_dtype <= SF_BF16, SF_EINVAL, "bad x dtype %d", x_dtype);
+  SF_REQUIRE(workspace_bytes >= sf_lm_head_workspace_bytes(V), SF_EINVAL,
+             "lm_head workspace too small: %zu < %zu", workspace_bytes,
+             sf_lm_head_workspace_bytes(V));
+  SF_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)workspace & 255) == 0, SF_EINVAL,
+             "weights must be 16-byte and workspace 256-byte aligned");
+  unsigned *counter = (unsigned *)workspace;
+  float *pv = (float *)((char *)workspace + 256);
+  int *pi = (int *)(pv + kHeadBlocks);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *wb = (const uint16_t *)w;
+  if (x_dtype == SF_F32)
+    k_lm_head_argmax<SF_F32><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
+                                                               pos_inc, hist, pv, pi, counter);
+  else if (x_dtype == SF_F16)
+    k_lm_head_argmax<SF_F16><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
+                                                               pos_inc, hist, pv, pi, counter);
+  else
+    k_lm_head_argmax<SF_BF16><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
+                                                                pos_inc, hist, pv, pi, counter);
+  return sf_check_launch("sf_lm_head_argmax");
+}

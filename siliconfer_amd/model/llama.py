@@ -1,0 +1,395 @@
+"""Decoder runner on MI355X — the reference's `LlamaModel` / `TransformerBlock`
+(/root/reference/siliconfer/model/llama.py:20-93,
+/root/reference/siliconfer/model/layers.py:72-163) with every projection an
+int4 `Q4Linear` weight and an int8 `QuantizedKVCache`, batch 1.
+
+The forward pass is the reference's, restated over this build's kernels:
+
+  embed -> per layer: RMSNorm -> q|k|v projection (+bias) -> RoPE + int8 KV
+  append -> attention over the int8 cache -> o projection + residual ->
+  RMSNorm -> gate|up projection -> silu(gate) * up -> down projection +
+  residual -> final RMSNorm -> tied-embedding logits -> greedy token.
+
+Differences of form, not of result:
+  * q/k/v and gate/up are each one fused int4 weight (rows concatenated; the
+    per-row groups quantize identically);
+  * the residual add after o / down rides in the GEMV as its bias (decode) or
+    in the next RMSNorm (prefill);
+  * the residual stream is fp32; projections run on `act_dtype` activations
+    (fp32 by default, like the reference's `Q4Linear`, which casts to fp32);
+  * decode positions and the greedy token stay on the device, so a decode
+    step is one HIP-graph replay with no host round trip (`capture`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .. import _lib
+from .._lib import SFError
+from ..kernels.q4 import Q4Weight
+from .config import ModelConfig, rope_tables
+
+_DT = {torch.float32: _lib.SF_F32, torch.float16: _lib.SF_F16, torch.bfloat16: _lib.SF_BF16}
+
+
+def pack_sym_device(W: torch.Tensor, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric RTN int4 of a device fp32 matrix, packed like
+    `siliconfer_amd.kernels.pack_weights_sym` (scale = max|w| / 7 per group,
+    q = clip(round(w / scale), -8, 7), low nibble = even column): returns
+    (packed uint8 [N, K/2], scales fp32 [N, K/g]) on the same device. Same
+    IEEE fp32 division and round-half-even as the numpy packer, so the codes
+    agree bit for bit."""
+    N, K = W.shape
+    if K % group_size:
+        raise SFError("in_features must be divisible by group_size")
+    g = W.float().reshape(N, K // group_size, group_size)
+    amax = g.abs().amax(dim=-1, keepdim=True)
+    # a tensor divisor: torch divides by a Python scalar through its reciprocal
+    scale = amax / torch.full_like(amax, 7.0)
+    safe = torch.where(scale == 0, torch.ones_like(scale), scale)
+    q = torch.round(g / safe).clamp_(-8, 7).to(torch.int8).reshape(N, K)
+    lo = q[:, 0::2].to(torch.uint8) & 0x0F
+    hi = q[:, 1::2].to(torch.uint8) & 0x0F
+    return (lo | (hi << 4)).contiguous(), scale[..., 0].contiguous()
+
+
+@dataclass
+class LayerWeights:
+    qkv: Q4Weight
+    qkv_bias: torch.Tensor | None  # fp32 [(H + 2 KVH) * D]
+    o: Q4Weight
+    gate_up: Q4Weight
+    down: Q4Weight
+    w_in: torch.Tensor    # fp32 [hidden]
+    w_post: torch.Tensor  # fp32 [hidden]
+
+
+@dataclass
+class GenerationResult:
+    token_ids: list[int]
+    prefill_time: float
+    decode_time: float
+    num_prefill_tokens: int
+    num_decode_tokens: int
+
+    @property
+    def prefill_tok_s(self) -> float:
+        return self.num_prefill_tokens / self.prefill_time if self.prefill_time else 0.0
+
+    @property
+    def decode_tok_s(self) -> float:
+        return self.num_decode_tokens / self.decode_time if self.decode_time else 0.0
+
+
+class LlamaModel:
+    """Batch-1 int4 decoder on one GPU. `max_seq` bounds prompt + generated
+    tokens (the KV cache capacity and the RoPE table)."""
+
+    def __init__(self, config: ModelConfig, layers: list[LayerWeights], embed: torch.Tensor,
+                 norm_w: torch.Tensor, group_size: int, max_seq: int,
+                 act_dtype: torch.dtype = torch.float32, max_prefill: int = 512):
+        if embed.dtype != torch.bfloat16:
+            raise SFError("the tied embedding must be bf16")
+        if act_dtype not in _DT:
+            raise SFError("act_dtype must be float32, float16 or bfloat16")
+        self.config, self.layers, self.embed, self.norm_w = config, layers, embed, norm_w
+        self.group_size, self.max_seq, self.act_dtype = group_size, max_seq, act_dtype
+        self.max_prefill = max_prefill
+        self.device = embed.device
+        self.lib = _lib.load()
+        c = config
+        self.H, self.Hq, self.KVH, self.D = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        self.I, self.V = c.intermediate_size, c.vocab_size
+        self.qkv_n = (self.Hq + 2 * self.KVH) * self.D
+        self.scale = float(self.D ** -0.5)
+        dev = self.device
+        f32 = torch.float32
+        # KV cache: per layer codes [KVH, T_cap, D] int8 and fp16 scales [KVH, T_cap]
+        self.k_codes = [torch.zeros((self.KVH, max_seq, self.D), dtype=torch.int8, device=dev) for _ in layers]
+        self.v_codes = [torch.zeros_like(t) for t in self.k_codes]
+        self.k_scales = [torch.zeros((self.KVH, max_seq), dtype=torch.float16, device=dev) for _ in layers]
+        self.v_scales = [torch.zeros_like(t) for t in self.k_scales]
+        cos, sin = rope_tables(config, max_seq)
+        self.cos = torch.from_numpy(cos).to(dev)
+        self.sin = torch.from_numpy(sin).to(dev)
+        # decode buffers
+        a = act_dtype
+        self.h = torch.zeros((1, self.H), dtype=f32, device=dev)
+        self.xn = torch.zeros((1, self.H), dtype=a, device=dev)
+        self.qkv = torch.zeros((1, self.qkv_n), dtype=f32, device=dev)
+        self.q = torch.zeros((1, self.Hq, self.D), dtype=a, device=dev)
+        self.attn = torch.zeros((1, self.Hq * self.D), dtype=a, device=dev)
+        self.gu = torch.zeros((1, 2 * self.I), dtype=f32, device=dev)
+        self.act = torch.zeros((1, self.I), dtype=a, device=dev)
+        self.logits = torch.zeros((self.V,), dtype=f32, device=dev)
+        self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.pos_dev = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.hist = torch.zeros((max_seq + 1,), dtype=torch.int32, device=dev)
+        self.attn_splits = int(self.lib.sf_attn_default_splits(1, self.KVH, max_seq))
+        ws = max(self.lib.sf_attn_workspace_bytes(1, self.Hq, self.D, self.attn_splits), 1 << 16)
+        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)   # counters start at zero
+        hw = self.lib.sf_lm_head_workspace_bytes(self.V)
+        self.head_ws = torch.zeros(hw, dtype=torch.uint8, device=dev)
+        self.pos = 0
+        self.graph = None
+        self._prefill_bufs = None
+        self._gemm_ws = None
+
+    # ------------------------------------------------------------------ init
+    @classmethod
+    def random_init(cls, config: ModelConfig, seed: int = 4, group_size: int = 64,
+                    device=None, max_seq: int = 1024, act_dtype: torch.dtype = torch.float32,
+                    std: float = 0.02, max_prefill: int = 512) -> "LlamaModel":
+        """Random weights N(0, std) drawn on the device from `seed` (RMSNorm
+        weights 1, q/k/v biases N(0, std) when the config has attention bias),
+        every projection RTN int4 symmetric with `group_size`, the tied
+        embedding in bf16."""
+        if not _lib.hip_available():
+            raise SFError("no gfx950 HIP device: siliconfer_amd has no CPU fallback")
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        c = config
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        Hq, KVH = c.num_attention_heads, c.num_key_value_heads
+
+        def randn(*shape):
+            return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std
+
+        def q4(*mats):
+            W = torch.cat(mats, dim=0) if len(mats) > 1 else mats[0]
+            pk, sc = pack_sym_device(W, group_size)
+            return Q4Weight(pk, sc, None, group_size, device=dev)
+
+        embed = randn(c.vocab_size, H).to(torch.bfloat16).contiguous()
+        layers = []
+        for _ in range(c.num_hidden_layers):
+            qkv = q4(randn(Hq * D, H), randn(KVH * D, H), randn(KVH * D, H))
+            bias = randn((Hq + 2 * KVH) * D) if c.attention_bias else None
+            o = q4(randn(H, Hq * D))
+            gate_up = q4(randn(I, H), randn(I, H))
+            down = q4(randn(H, I))
+            ones = torch.ones(H, dtype=torch.float32, device=dev)
+            layers.append(LayerWeights(qkv, bias, o, gate_up, down, ones, ones.clone()))
+        norm_w = torch.ones(H, dtype=torch.float32, device=dev)
+        return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill)
+
+    def export_weights(self) -> dict:
+        """Host copies for a reference restatement: dequantized fp32 weights
+        (fp16 scales as stored), biases, norms, the embedding as fp32."""
+        out = {"embed": self.embed.float().cpu().numpy(), "norm": self.norm_w.cpu().numpy(),
+               "layers": []}
+        for L in self.layers:
+            d = {}
+            for name in ("qkv", "o", "gate_up", "down"):
+                w: Q4Weight = getattr(L, name)
+                pk, s, _ = w.canonical()
+                pk = pk.cpu().numpy()
+                s = s.float().cpu().numpy()
+                lo = (pk & 0x0F).astype(np.int16)
+                hi = (pk >> 4).astype(np.int16)
+                q = np.empty((pk.shape[0], pk.shape[1] * 2), np.int16)
+                q[:, 0::2], q[:, 1::2] = lo, hi
+                q = np.where(q > 7, q - 16, q).astype(np.float32)
+                g = self.group_size
+                d[name] = (q.reshape(q.shape[0], -1, g) * s[..., None]).reshape(q.shape)
+            d["qkv_bias"] = None if L.qkv_bias is None else L.qkv_bias.cpu().numpy()
+            d["w_in"], d["w_post"] = L.w_in.cpu().numpy(), L.w_post.cpu().numpy()
+            out["layers"].append(d)
+        return out
+
+    # ------------------------------------------------------------- launches
+    def _st(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _chk(self, rc, what):
+        _lib.check(rc, what)
+
+    def _gemv(self, w: Q4Weight, x: torch.Tensor, y32: torch.Tensor, bias: torch.Tensor | None):
+        self._chk(self.lib.sf_q4_gemv(w.blob.data_ptr(), x.data_ptr(), _DT[x.dtype], None, _lib.SF_F32,
+                                      y32.data_ptr(), None if bias is None else bias.data_ptr(),
+                                      _lib.SF_F32, 1, w.out_features, w.in_features, w.group_size,
+                                      int(w.has_zeros), self._st()), "sf_q4_gemv")
+
+    def _gemm(self, w: Q4Weight, X: torch.Tensor, Y32: torch.Tensor, bias: torch.Tensor | None):
+        M = X.shape[0]
+        need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features, w.group_size)
+        if need and (self._gemm_ws is None or self._gemm_ws.numel() < need):
+            self._gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        ws = self._gemm_ws if need else None
+        self._chk(self.lib.sf_q4_gemm(w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], None, _lib.SF_F32,
+                                      Y32.data_ptr(), None if bias is None else bias.data_ptr(),
+                                      _lib.SF_F32, M, w.out_features, w.in_features, w.group_size,
+                                      int(w.has_zeros), None if ws is None else ws.data_ptr(),
+                                      0 if ws is None else ws.numel(), self._st()), "sf_q4_gemm")
+
+    def _rmsnorm(self, x, delta, w, out, rows):
+        self._chk(self.lib.sf_rmsnorm(x.data_ptr(), None if delta is None else delta.data_ptr(),
+                                      w.data_ptr(), _lib.SF_F32, out.data_ptr(), _DT[out.dtype], rows,
+                                      self.H, float(self.config.rms_norm_eps), self._st()), "sf_rmsnorm")
+
+    def _rope_append(self, l, qkv, q_out, rows, pos_dev, pos_host):
+        self._chk(self.lib.sf_rope_kv_append(
+            qkv.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(), self.max_seq, q_out.data_ptr(),
+            _DT[q_out.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
+            self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, rows, self.Hq,
+            self.KVH, self.D, self.max_seq, pos_dev, pos_host, self._st()), "sf_rope_kv_append")
+
+    def _lm_head(self, x_row, token, pos_inc, logits=True):
+        self._chk(self.lib.sf_lm_head_argmax(
+            self.embed.data_ptr(), x_row.data_ptr(), _DT[x_row.dtype],
+            self.logits.data_ptr() if logits else None, self.V, self.H, token.data_ptr(),
+            pos_inc, self.hist.data_ptr() if pos_inc else None, self.head_ws.data_ptr(),
+            self.head_ws.numel(), self._st()), "sf_lm_head_argmax")
+
+    # --------------------------------------------------------------- prefill
+    def reset(self) -> None:
+        """Empty the KV cache (positions restart at 0; codes are overwritten)."""
+        self.pos = 0
+        self.pos_dev.zero_()
+
+    def _bufs(self, T):
+        if self._prefill_bufs is None or self._prefill_bufs["T"] < T:
+            dev, a, f32 = self.device, self.act_dtype, torch.float32
+            self._prefill_bufs = dict(
+                T=T, H=torch.empty((T, self.H), dtype=f32, device=dev),
+                Xn=torch.empty((T, self.H), dtype=a, device=dev),
+                QKV=torch.empty((T, self.qkv_n), dtype=f32, device=dev),
+                Q=torch.empty((T, self.Hq, self.D), dtype=a, device=dev),
+                A=torch.empty((T, self.Hq * self.D), dtype=a, device=dev),
+                Dl=torch.empty((T, self.H), dtype=f32, device=dev),
+                GU=torch.empty((T, 2 * self.I), dtype=f32, device=dev),
+                ACT=torch.empty((T, self.I), dtype=a, device=dev),
+                ids=torch.empty((T,), dtype=torch.int32, device=dev))
+        return self._prefill_bufs
+
+    def prefill(self, ids, want_logits: bool = True) -> int:
+        """Run the prompt (appending to the cache) and return the greedy next
+        token; `self.logits` holds the last row's logits."""
+        ids = np.asarray(ids, dtype=np.int64).reshape(-1)
+        T = int(ids.size)
+        if T == 0:
+            raise SFError("empty prompt")
+        if ids.min() < 0 or ids.max() >= self.V:
+            raise SFError("token id out of range")
+        if self.pos + T > self.max_seq:
+            raise SFError(f"prompt of {T} tokens exceeds the cache capacity {self.max_seq}")
+        done = 0
+        while done < T:  # chunks of at most max_prefill rows
+            n = min(self.max_prefill, T - done)
+            self._prefill_chunk(ids[done:done + n], want_logits and done + n == T)
+            done += n
+        return int(self.token.item())
+
+    def _prefill_chunk(self, ids: np.ndarray, want_logits: bool):
+        T = int(ids.size)
+        b = self._bufs(T)
+        Hb, Xn, QKV, Q, A, Dl, GU, ACT = (b[k][:T] for k in ("H", "Xn", "QKV", "Q", "A", "Dl", "GU", "ACT"))
+        idt = b["ids"][:T]
+        idt.copy_(torch.from_numpy(ids.astype(np.int32)))
+        lib, st = self.lib, self._st()
+        self._chk(lib.sf_embed(idt.data_ptr(), self.embed.data_ptr(), _lib.SF_BF16, Hb.data_ptr(), T,
+                               self.H, self.V, st), "sf_embed")
+        for l, L in enumerate(self.layers):
+            self._rmsnorm(Hb, None if l == 0 else Dl, L.w_in, Xn, T)
+            self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
+            self._rope_append(l, QKV, Q, T, None, self.pos)
+            self._chk(lib.sf_attn_prefill_i8kv(
+                Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
+                self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, A.data_ptr(),
+                _DT[A.dtype], T, self.Hq, self.KVH, self.pos, self.max_seq, self.D, self.scale, st),
+                "sf_attn_prefill_i8kv")
+            self._gemm(L.o, A, Dl, None)
+            self._rmsnorm(Hb, Dl, L.w_post, Xn, T)
+            self._gemm(L.gate_up, Xn, GU, None)
+            self._chk(lib.sf_silu_mul(GU.data_ptr(), ACT.data_ptr(), _DT[ACT.dtype], T, self.I, st),
+                      "sf_silu_mul")
+            self._gemm(L.down, ACT, Dl, None)
+        self._rmsnorm(Hb, Dl, self.norm_w, Xn, T)
+        self._lm_head(Xn[T - 1], self.token, None, logits=want_logits)
+        self.pos += T
+        self.pos_dev.fill_(self.pos)
+
+    # ---------------------------------------------------------------- decode
+    def decode_step(self, logits: bool = False) -> None:
+        """One greedy decode step on the device: embeds `self.token` at
+        position p = `pos_dev`, writes the next token to `self.token` and
+        `self.hist[p]`, increments `pos_dev`. No host synchronisation."""
+        lib, st = self.lib, self._st()
+        pos = self.pos_dev.data_ptr()
+        self._chk(lib.sf_embed(self.token.data_ptr(), self.embed.data_ptr(), _lib.SF_BF16,
+                               self.h.data_ptr(), 1, self.H, self.V, st), "sf_embed")
+        for l, L in enumerate(self.layers):
+            self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
+            self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
+            self._rope_append(l, self.qkv, self.q, 1, pos, 0)
+            self._chk(lib.sf_attn_decode_i8kv_dev(
+                self.q.data_ptr(), _DT[self.q.dtype], self.k_codes[l].data_ptr(),
+                self.k_scales[l].data_ptr(), self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(),
+                _lib.SF_F16, self.attn.data_ptr(), _DT[self.attn.dtype], self.attn_ws.data_ptr(),
+                self.attn_ws.numel(), 1, self.Hq, self.KVH, pos, 1, self.max_seq, self.max_seq,
+                self.D, self.scale, self.attn_splits, st), "sf_attn_decode_i8kv_dev")
+            self._gemv(L.o, self.attn, self.h, self.h)        # residual add as the bias
+            self._rmsnorm(self.h, None, L.w_post, self.xn, 1)
+            self._gemv(L.gate_up, self.xn, self.gu, None)
+            self._chk(lib.sf_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), _DT[self.act.dtype], 1,
+                                      self.I, st), "sf_silu_mul")
+            self._gemv(L.down, self.act, self.h, self.h)
+        self._rmsnorm(self.h, None, self.norm_w, self.xn, 1)
+        self._lm_head(self.xn, self.token, pos, logits=logits)
+
+    def capture(self, logits: bool = False) -> None:
+        """Record one decode step as a HIP graph (positions and tokens are
+        device-side, so every replay advances the sequence by one token).
+        Capturing launches nothing; the step contains no memset."""
+        torch.cuda.synchronize(self.device)
+        s = torch.cuda.Stream(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self.decode_step(logits=logits)
+        torch.cuda.synchronize(self.device)
+        self.graph = g
+
+    def replay(self, n: int = 1) -> None:
+        if self.graph is None:
+            raise SFError("capture() first")
+        if self.pos + n > self.max_seq:
+            raise SFError("decode would exceed the cache capacity")
+        for _ in range(n):
+            self.graph.replay()
+        self.pos += n
+
+    # -------------------------------------------------------------- generate
+    def generate(self, prompt_ids, max_tokens: int = 128, use_graph: bool = True) -> GenerationResult:
+        """Greedy generation (the reference's `generate` at temperature 0,
+        engine/generate.py:117-180): prefill, then max_tokens - 1 decode steps.
+        Decode time covers the steps after the first token, as there."""
+        import time
+        self.reset()
+        torch.cuda.synchronize(self.device)
+        t0 = time.perf_counter()
+        first = self.prefill(prompt_ids)
+        t1 = time.perf_counter()
+        n = max_tokens - 1
+        if self.pos + n > self.max_seq:
+            raise SFError("prompt + max_tokens exceeds the cache capacity")
+        if use_graph and self.graph is None:
+            raise SFError("capture() before generate(use_graph=True)")
+        start = self.pos
+        t2 = time.perf_counter()
+        if use_graph:
+            self.replay(n)
+        else:
+            for _ in range(n):
+                self.decode_step()
+            self.pos += n
+        torch.cuda.synchronize(self.device)
+        t3 = time.perf_counter()
+        # the step at position p wrote its output token to hist[p]
+        toks = [first] + (self.hist[start:start + n].cpu().tolist() if n > 0 else [])
+        return GenerationResult(toks, t1 - t0, t3 - t2, int(np.asarray(prompt_ids).size), n)

@@ -1,0 +1,150 @@
+"""End-to-end decoder on the GPU against the numpy oracle
+of the reference's forward pass (oracle/model.py, restating
+/root/reference/siliconfer/model/layers.py, llama.py and the greedy branch of
+engine/generate.py).
+
+Tolerances: logits are compared norm-relative. The GPU path and the oracle
+both compute in fp32 but sum in different orders; an int8 KV code can then
+land on the other side of a rounding boundary (one code step, 1/127 of a
+row's max), which moves scores by that much — hence 2e-3 for the 2-layer
+model and 1e-2 after 24 layers. Greedy tokens must agree whenever the
+oracle's top-2 margin exceeds the logit tolerance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as OM
+from oracle.linear import assert_close
+from siliconfer_amd.model.config import ModelConfig, rope_tables
+from siliconfer_amd.model.llama import LlamaModel, pack_sym_device
+
+pytestmark = pytest.mark.gpu
+
+SMALL = ModelConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                    num_attention_heads=4, num_key_value_heads=2, head_dim=64, vocab_size=1000,
+                    rms_norm_eps=1e-6, rope_theta=1e6, tie_word_embeddings=True,
+                    attention_bias=True)
+
+
+def margin_ok(logits: np.ndarray, tol: float) -> bool:
+    top2 = np.sort(logits)[-2:]
+    return (top2[1] - top2[0]) > tol * np.linalg.norm(logits) / np.sqrt(logits.size) * 10
+
+
+def check_against_oracle(m: LlamaModel, cfg, ids, n_decode, tol, what):
+    W = m.export_weights()
+    cos, sin = rope_tables(cfg, m.max_seq)
+    cache = OM.KVCache(cfg.num_hidden_layers)
+    m.reset()
+    tok = m.prefill(ids)
+    ref = OM.forward(W, cfg, ids, cache, cos, sin)[-1]
+    got = m.logits.cpu().numpy()
+    assert_close(got, ref, tol, f"{what} prefill logits")
+    if margin_ok(ref, tol):
+        assert tok == OM.greedy(ref), f"{what}: prefill token"
+    for i in range(n_decode):
+        m.decode_step(logits=True)
+        torch.cuda.synchronize()
+        ref = OM.forward(W, cfg, [tok], cache, cos, sin)[-1]
+        got = m.logits.cpu().numpy()
+        assert_close(got, ref, tol, f"{what} decode step {i} logits")
+        nxt = int(m.token.item())
+        if margin_ok(ref, tol):
+            assert nxt == OM.greedy(ref), f"{what}: decode step {i} token"
+        tok = nxt
+        m.pos += 1
+    assert int(m.pos_dev.item()) == m.pos
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.float16])
+def test_small_model_matches_oracle(dev, act):
+    m = LlamaModel.random_init(SMALL, seed=11, group_size=64, device=dev, max_seq=64, act_dtype=act)
+    ids = np.random.default_rng(12).integers(0, SMALL.vocab_size, 13)
+    tol = 2e-3 if act == torch.float32 else 1e-2
+    check_against_oracle(m, SMALL, ids, 6, tol, f"small/{act}")
+
+
+def test_prefill_in_chunks_equals_one_prefill(dev):
+    a = LlamaModel.random_init(SMALL, seed=13, device=dev, max_seq=64)
+    b = LlamaModel.random_init(SMALL, seed=13, device=dev, max_seq=64, max_prefill=5)
+    ids = np.random.default_rng(14).integers(0, SMALL.vocab_size, 17)
+    ta, tb = a.prefill(ids), b.prefill(ids)
+    assert_close(b.logits.cpu().numpy(), a.logits.cpu().numpy(), 1e-4, "chunked prefill")
+    assert ta == tb
+
+
+def test_graph_replay_equals_eager(dev):
+    m = LlamaModel.random_init(SMALL, seed=15, device=dev, max_seq=64)
+    ids = np.random.default_rng(16).integers(0, SMALL.vocab_size, 9)
+    m.prefill(ids)
+    start = m.pos
+    for _ in range(10):
+        m.decode_step(logits=True)
+    m.pos += 10
+    torch.cuda.synchronize()
+    eager_toks = m.hist[start:start + 10].cpu().clone()
+    eager_logits = m.logits.cpu().clone()
+    m.reset()
+    m.prefill(ids)
+    m.capture(logits=True)
+    for r in range(10):  # replays with eager work and synchronisation between them
+        m.replay(1)
+        torch.cuda.synchronize()
+        assert int(m.pos_dev.item()) == start + r + 1
+    assert torch.equal(m.hist[start:start + 10].cpu(), eager_toks)
+    assert torch.equal(m.logits.cpu(), eager_logits)
+
+
+def test_generate_result(dev):
+    m = LlamaModel.random_init(SMALL, seed=17, device=dev, max_seq=64)
+    m.capture()
+    ids = np.random.default_rng(18).integers(0, SMALL.vocab_size, 20)
+    r = m.generate(ids, max_tokens=12)
+    assert len(r.token_ids) == 12 and r.num_decode_tokens == 11 and r.num_prefill_tokens == 20
+    assert r.decode_tok_s > 0 and r.prefill_tok_s > 0
+    r2 = m.generate(ids, max_tokens=12, use_graph=False)
+    assert r2.token_ids == r.token_ids
+    # greedy continuation equals feeding the generated tokens back one at a time
+    m.reset()
+    m.prefill(ids)
+    for t in r.token_ids[:-1]:
+        m.token.fill_(t)
+        m.decode_step()
+        m.pos += 1
+    assert int(m.token.item()) == r.token_ids[-1]
+
+
+def test_capacity_and_id_checks(dev):
+    from siliconfer_amd._lib import SFError
+
+    m = LlamaModel.random_init(SMALL, seed=19, device=dev, max_seq=16)
+    with pytest.raises(SFError):
+        m.prefill(np.arange(17) % 100)
+    with pytest.raises(SFError):
+        m.prefill([SMALL.vocab_size])
+    m.capture()
+    m.prefill(np.arange(15))
+    with pytest.raises(SFError):
+        m.replay(2)
+
+
+def test_device_packer_matches_numpy_packer(dev):
+    from siliconfer_amd.kernels import pack_weights_sym
+
+    rng = np.random.default_rng(20)
+    W = rng.normal(0, 0.02, (64, 512)).astype(np.float32)
+    pk, s = pack_weights_sym(W, 64)
+    tpk, ts = pack_sym_device(torch.as_tensor(W).to(dev), 64)
+    np.testing.assert_array_equal(tpk.cpu().numpy(), pk)
+    np.testing.assert_array_equal(ts.cpu().numpy(), s)
+
+
+def test_qwen05b_geometry_matches_oracle(dev):
+    """BASELINE config 5 geometry (24 layers, 14/2 heads, vocab 151936): a
+    32-token prompt and 3 decode steps against the oracle."""
+    cfg = ModelConfig.qwen25_05b()
+    m = LlamaModel.random_init(cfg, seed=4, group_size=64, device=dev, max_seq=64)
+    ids = np.random.default_rng(4).integers(0, cfg.vocab_size, 32)
+    check_against_oracle(m, cfg, ids, 3, 1e-2, "qwen0.5b")
