@@ -19,6 +19,16 @@ Printed JSON (one line):
                 rocprofv3 FETCH_SIZE + WRITE_SIZE counters measured
                 (profiles/gemv_sweep_pmc.json, calibrated on a copy of known
                 size), when that file is present;
+  decode_tok_s  BASELINE config 5, the metric's second half: greedy decode on a
+                random-init Qwen2.5-0.5B-geometry model (all projections int4
+                sym g=64, int8 KV, bf16 tied embedding), 512 random prompt ids,
+                256 tokens, batch 1; fp32 residual stream, projections fed
+                fp16 activations (RNE from fp32: each projection stays within
+                the 1e-3 bar against the reference's fp32 Q4Linear); decode
+                steps are HIP-graph replays; median of 3. `e2e_config5` has
+                the details (fp32-activation projections too, prefill time,
+                the lm_head's share, bytes per token and the HBM roofline,
+                and the numpy restatement on the host cores);
   secondary     the other hot-path kernels at their BASELINE configs, timed the
                 same way: config-1 GEMV, config-2 prefill GEMM, config-4
                 decode attention, the KV-cache append;
@@ -31,8 +41,9 @@ Printed JSON (one line):
 Algorithmic bytes per launch (B = batch): N*K/2 (int4) + 2*N*K/128 (fp16
 scales) + 2*B*K (fp16 x) + 2*B*N (fp16 y).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
        python bench.py --profile-kernels   (eager launches for rocprofv3 runs)
+       python bench.py --profile-e2e       (eager config-5 decode steps for rocprofv3)
 """
 
 from __future__ import annotations
@@ -259,6 +270,91 @@ def secondary(dev, stream, eager=False):
     return out
 
 
+E2E_PROMPT, E2E_TOKENS = 512, 256
+
+
+def e2e_model(dev, act):
+    from siliconfer_amd.model.config import ModelConfig
+    from siliconfer_amd.model.llama import LlamaModel
+
+    cfg = ModelConfig.qwen25_05b()
+    m = LlamaModel.random_init(cfg, seed=4, group_size=64, device=dev,
+                               max_seq=E2E_PROMPT + E2E_TOKENS + 256, act_dtype=act)
+    ids = np.random.default_rng(4).integers(0, cfg.vocab_size, E2E_PROMPT)
+    return cfg, m, ids
+
+
+def e2e_decode(dev, runs: int = 3):
+    """random-init Qwen2.5-0.5B geometry, every projection
+    int4 sym g=64, int8 KV, 512 uniformly random prompt ids, 256 greedy tokens,
+    batch 1; decode tok/s = 255 decode steps (HIP-graph replays) / their time,
+    median of `runs` after a warmup generation (the reference's
+    GenerationResult.decode_tok_s)."""
+    import torch
+
+    out = {}
+    for name, act in (("fp16", torch.float16), ("fp32", torch.float32)):
+        cfg, m, ids = e2e_model(dev, act)
+        m.capture()
+        m.generate(ids, 16)
+        rs = [m.generate(ids, E2E_TOKENS) for _ in range(runs)]
+        order = sorted(range(runs), key=lambda i: rs[i].decode_tok_s)
+        med = rs[order[runs // 2]]
+        timer = Timer(torch, torch.cuda.Stream(dev))
+        head_us = timer.per_call_us([lambda: m._lm_head(m.xn, m.token, None, logits=False)] * 32)
+        w_bytes = sum(getattr(L, n).nbytes for L in m.layers for n in ("qkv", "o", "gate_up", "down"))
+        head_bytes = m.embed.numel() * 2
+        T_mean = E2E_PROMPT + E2E_TOKENS / 2
+        kv_bytes = cfg.num_hidden_layers * 2 * cfg.num_key_value_heads * T_mean * (cfg.head_dim + 2)
+        per_tok = w_bytes + head_bytes + kv_bytes
+        ms = 1e3 / med.decode_tok_s
+        out[name] = {
+            "decode_tok_s": round(med.decode_tok_s, 1),
+            "runs_tok_s": [round(r.decode_tok_s, 1) for r in rs],
+            "ms_per_token": round(ms, 4),
+            "prefill_ms_512": round(med.prefill_time * 1e3, 3),
+            "lm_head_us": round(head_us, 2),
+            "lm_head_share": round(head_us * 1e-3 / ms, 4),
+            "hbm_bytes_per_token": int(per_tok),
+            "hbm_GBps": round(per_tok / (ms * 1e-3) / 1e9, 1),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
+            "first_tokens": med.token_ids[:8],
+        }
+        del m
+        torch.cuda.empty_cache()
+    out["launches_per_token"] = 2 + 9 * cfg.num_hidden_layers + 1
+    return out
+
+
+def e2e_cpu_baseline(dev, budget_s: float):
+    """The numpy restatement of the forward pass (oracle/model.py) on the host
+    cores, same weights: a 512-token prompt, then decode steps for about
+    `budget_s` seconds."""
+    import torch
+
+    from oracle import model as OM
+    from siliconfer_amd.model.config import rope_tables
+
+    cfg, m, ids = e2e_model(dev, torch.float32)
+    W = m.export_weights()
+    cos, sin = rope_tables(cfg, m.max_seq)
+    del m
+    torch.cuda.empty_cache()
+    cache = OM.KVCache(cfg.num_hidden_layers)
+    t0 = time.perf_counter()
+    tok = OM.greedy(OM.forward(W, cfg, ids, cache, cos, sin)[-1])
+    t_prefill = time.perf_counter() - t0
+    n, t1 = 0, time.perf_counter()
+    while time.perf_counter() - t1 < budget_s and n < E2E_TOKENS - 1:
+        tok = OM.greedy(OM.forward(W, cfg, [tok], cache, cos, sin)[-1])
+        n += 1
+    dt = time.perf_counter() - t1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps after the 512-token prompt ({t_prefill:.1f} s), "
+                      "numpy fp32 over the dequantized int4 weights and the int8 cache"}
+
+
 def cpu_baseline(budget_s: float):
     """Reference CPU kernel on a bounded sample of the same sweep."""
     from oracle import cpu
@@ -409,6 +505,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other kernels' timings")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end decode")
+    ap.add_argument("--profile-e2e", action="store_true",
+                    help="only run eager config-5 decode steps (for rocprofv3)")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of reference CPU work")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -438,6 +537,14 @@ def main() -> int:
     if args.profile_kernels:
         profile_kernels(dev)
         return 0
+    if args.profile_e2e:
+        _, m, ids = e2e_model(dev, torch.float32)
+        m.prefill(ids)
+        for _ in range(8):
+            m.decode_step()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_e2e": "prefill 512 + 8 eager decode steps, fp32 activations"}))
+        return 0
 
     sweep = GpuSweep(dev)
     if not args.eager:
@@ -466,6 +573,9 @@ def main() -> int:
              for (N, K, B, *_), t, b in zip(sweep.cases, us, case_bytes)]
     traffic, _ = load_traffic()
     sec = None if args.no_secondary else secondary(dev, sweep.stream)
+    e2e = None if args.no_e2e else e2e_decode(dev)
+    if e2e is not None and not args.no_cpu:
+        e2e["cpu_baseline"] = e2e_cpu_baseline(dev, args.cpu_budget)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
 
     line = {
@@ -499,6 +609,8 @@ def main() -> int:
             "alg_bytes_per_launch_avg": int(sum(case_bytes) / len(case_bytes)),
         },
         "cases": cases,
+        "decode_tok_s": None if e2e is None else e2e["fp16"]["decode_tok_s"],
+        "e2e_config5": e2e,
         "secondary": sec,
         "cpu_baseline": cpu,
     }
