@@ -2,6 +2,8 @@
 #include "q4_gemv_kernel.h"
 
 namespace sf_gemv {
+bool mfma_gemv_applies(int B, int K, int g, int xdt);
+int launch_mfma_gemv(const GemvArgs &a, int g);
 extern template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_BF16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
@@ -37,7 +39,14 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
   const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
   GemvArgs args{w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, L.G, has_zeros != 0,
                 (hipStream_t)stream};
-  if (x_dtype == SF_F16) {
+  // batch 4..8 with fp16 activations: the MFMA kernel (SF_GEMV_MFMA=0 keeps the VALU one)
+  static const bool mfma_ok = [] {
+    const char *e = getenv("SF_GEMV_MFMA");
+    return !(e && e[0] == '0');
+  }();
+  if (mfma_ok && mfma_gemv_applies(B, K, group_size, x_dtype)) {
+    launch_mfma_gemv(args, group_size);
+  } else if (x_dtype == SF_F16) {
     launch_x<SF_F16>(pl, args);
   } else if (x_dtype == SF_BF16) {
     launch_x<SF_BF16>(pl, args);

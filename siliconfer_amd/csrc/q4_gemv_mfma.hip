@@ -1,0 +1,229 @@
+// q4_gemv_mfma.hip — int4 decode GEMV for small batches with fp16 activations
+// on MFMA (gfx950); same result contract as the VALU GEMV (q4_gemv_kernel.h).
+//
+// Why MFMA here: the VALU GEMV spends one dot2 per two weights per batch row,
+// so from batch 4 up its arithmetic, and the batch rows of activations every
+// lane holds, make it VALU- and register-bound instead of HBM-bound. On MFMA
+// (v_mfma_f32_16x16x32_f16) the batch is the M side of the A operand (rows
+// >= B read a valid row and only feed output rows that are never stored), each
+// weight is dequantized once to an exact fp16 integer (q - z), and a lane needs
+// 16 bytes of activations per MFMA.
+//
+// Layout: one workgroup per 16 weight rows; wave w covers the K blocks
+// [w * BPW, (w + 1) * BPW). A block is one scale group: lane l (row
+// n = l % 16, k-group kg = l / 16) loads LW bytes of row n per block, LW = 16
+// for group size 128 (four MFMAs per load) and 8 for group size 64 (two). The
+// wider load halves the cache lines a wave instruction touches per byte: the
+// MFMA operand layout puts a different row in each of 16 consecutive lanes, so
+// one instruction reads 16 rows x 4 LW bytes.
+// Load order per wave: the first activation blocks, every group's scale (and
+// zero-point) bits, then every weight block, so nothing the first MFMAs need
+// queues behind the weights (the load counter retires in issue order). The
+// MFMA's k order inside a lane is the order the nibble magic produces
+// (k0, k4, k1, k5, k2, k6, k3, k7); the activations are permuted to match,
+// which leaves the dot product unchanged. Each group's partial is scaled by its
+// fp16 scale in fp32 (exact weights, fp32 sums) and the waves' partials are
+// summed through LDS in wave order. Blocks per wave (BPW) is compile-time, so
+// group boundaries cost no selects and every register array stays in
+// registers.
+#include "q4_gemv_kernel.h"
+
+namespace {
+
+using sf_gemv::and_or;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTileN = 16;
+constexpr int kMaxWaves = 8;
+
+// Per-lane weight load width LW (bytes): 16 when a group spans 128 k, else 8.
+// A block is the K a wave instruction covers: 16 rows x (4 lanes x LW bytes),
+// i.e. 8 LW k, LW / 4 MFMAs.
+template <int LW> struct WLoad;
+template <> struct WLoad<8> { typedef u32x2 T; static constexpr int kMaxBpw = 24; };
+template <> struct WLoad<16> { typedef u32x4 T; static constexpr int kMaxBpw = 12; };
+
+template <int LW, bool ASYM, int BPW>
+__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 3)))
+k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
+               const uint8_t *__restrict__ ztile, const f16 *__restrict__ x, void *__restrict__ y,
+               int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt, int B,
+               int N, int K, int G, int nblk) {
+  constexpr int KB = 8 * LW;   // k per block
+  constexpr int NM = LW / 4;   // MFMAs per block (one per weight dword)
+  // activation ring: every block when they fit in 64 registers, else XR blocks
+  // loaded XR - 1 ahead
+  constexpr int XR = BPW * NM <= 16 ? BPW : 16 / NM;
+  constexpr int XPRE = XR == BPW ? BPW : XR - 1;
+  typedef typename WLoad<LW>::T wvec_t;
+  __shared__ float red[kMaxWaves][8][kTileN];
+
+  const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nl = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * kTileN;
+  const int n = min(n0 + nl, N - 1);  // rows past N re-read row N-1; never stored
+  const int blk0 = wave * BPW;        // the host launches only waves with blk0 < nblk
+  const int cnt = min(BPW, nblk - blk0);
+  const int blast = blk0 + cnt - 1;   // blocks past the wave's own re-read its last one
+  const int Kh = K >> 1;
+
+  // lane (row n, k-group kg) covers k = KB blk + 2 LW kg .. + 2 LW - 1 of each block
+  const f16 *xr = x + (size_t)min(nl, B - 1) * K + kg * 2 * LW;
+  u32x4 xs[XR][NM];
+  auto xload = [&](int i) {
+    const u32x4 *xq = (const u32x4 *)(xr + (size_t)min(blk0 + i, blast) * KB);
+#pragma unroll
+    for (int j = 0; j < NM; ++j) xs[i % XR][j] = xq[j];
+  };
+#pragma unroll
+  for (int i = 0; i < XPRE; ++i) xload(i);
+
+  uint32_t sbits[BPW], zbits[BPW];  // one group per block
+  {
+    const size_t cell0 = (size_t)(n >> 3) * G;
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+      const size_t cell = cell0 + min(blk0 + q, G - 1);
+      sbits[q] = ((const uint16_t *)stile)[cell * 8 + (n & 7)];
+      if constexpr (ASYM) zbits[q] = ztile[cell * 4 + ((n & 7) >> 1)];
+    }
+  }
+
+  wvec_t wv[BPW];
+  const uint8_t *wrow = w + (size_t)n * Kh + kg * LW;
+#pragma unroll
+  for (int i = 0; i < BPW; ++i)
+    wv[i] = __builtin_nontemporal_load((const wvec_t *)(wrow + (size_t)min(blk0 + i, blast) * 4 * LW));
+  // keep every load above issued before any math (the scheduler would otherwise
+  // interleave them with the MFMAs to save registers)
+  __builtin_amdgcn_sched_barrier(0);
+
+  const half2_t sixteenth = {(f16)0.0625f, (f16)0.0625f};
+  const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  float4_t part = zero4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // C rows b = 4 kg + r, column n
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    if (i + XPRE < BPW) xload(i + XPRE);
+    // blocks i >= cnt (only in a workgroup's last wave) are computed on re-read
+    // data and dropped at the scale step by a select: a branch here would let
+    // the compiler sink this block's loads into it, after the wait
+    uint32_t z = 8u;  // offset-binary symmetric codes
+    if constexpr (ASYM) {
+      uint32_t zb = zbits[i];
+      asm volatile("" : "+v"(zb));  // use the loaded bits here, not right after the load
+      z = (zb >> (4 * (n & 1))) & 15u;
+    }
+    const half2_t c1 = sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);        // -(1024 + z)
+    const half2_t c2 = sf_bitcast<half2_t>((0xD400u + 16u * z) * 0x10001u);  // -(64 + z)
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      // A: x[k0, k4, k1, k5, k2, k6, k3, k7] of this lane's j-th 8-k group
+      const u32x4 xv = xs[i % XR][j];
+      const half2_t p0 = sf_bitcast<half2_t>(xv.x), p1 = sf_bitcast<half2_t>(xv.y);
+      const half2_t p2 = sf_bitcast<half2_t>(xv.z), p3 = sf_bitcast<half2_t>(xv.w);
+      const half8_t a = half8_t{p0.x, p2.x, p0.y, p2.y, p1.x, p3.x, p1.y, p3.y};
+      // B: the same 8 weights, q - z exact in fp16
+      const uint32_t d = wv[i][j], d8 = d >> 8;
+      const half2_t v0 = sf_bitcast<half2_t>(and_or(d, 0x000F000Fu, 0x64006400u)) + c1;
+      const half2_t v1 = sf_bitcast<half2_t>(and_or(d, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
+      const half2_t v2 = sf_bitcast<half2_t>(and_or(d8, 0x000F000Fu, 0x64006400u)) + c1;
+      const half2_t v3 = sf_bitcast<half2_t>(and_or(d8, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
+      const half8_t bw = half8_t{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+      part = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, j == 0 ? zero4 : part,
+                                                    0, 0, 0);
+    }
+    {
+      uint32_t sb = sbits[i];
+      asm volatile("" : "+v"(sb));  // convert at the point of use (keeps the load in flight)
+      const float s = (float)sf_bitcast<f16>((uint16_t)sb);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = i < cnt ? fmaf(part[r], s, acc[r]) : acc[r];
+    }
+  }
+
+  // fold the waves (wave order) and store
+  if (kg < 2) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * kg + r][nl] = acc[r];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < B * kTileN; t += blockDim.x) {
+    const int b = t / kTileN, c = t - b * kTileN;
+    const int row = n0 + c;
+    if (row >= N) continue;
+    float v = 0.f;
+    for (int wi = 0; wi < nw; ++wi) v += red[wi][b][c];
+    sf_gemv::store_out(y, ydt, y32, bias, bdt, (size_t)b * N + row, row, v);
+  }
+}
+
+template <int LW, bool ASYM, int BPW>
+void launch_one(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk) {
+  k_q4_gemv_mfma<LW, ASYM, BPW><<<grid, nw * 64, 0, a.s>>>(
+      a.w, a.st, a.zt, (const f16 *)a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G,
+      nblk);
+}
+
+// Compiled blocks-per-wave counts: 8-byte lanes {2, 4, 8, 12, 16, 24},
+// 16-byte lanes {1, 2, 4, 6, 8, 12} (the same K per wave).
+template <int LW> constexpr int kBucket[6] = {2, 4, 8, 12, 16, 24};
+template <> constexpr int kBucket<16>[6] = {1, 2, 4, 6, 8, 12};
+
+template <int LW, bool ASYM>
+void launch_bpw(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int bpw) {
+  constexpr const int *bk = kBucket<LW>;
+#define SF_MB(I) launch_one<LW, ASYM, bk[I]>(a, grid, nw, nblk)
+  if (bpw == bk[0]) SF_MB(0);
+  else if (bpw == bk[1]) SF_MB(1);
+  else if (bpw == bk[2]) SF_MB(2);
+  else if (bpw == bk[3]) SF_MB(3);
+  else if (bpw == bk[4]) SF_MB(4);
+  else SF_MB(5);
+#undef SF_MB
+}
+
+}  // namespace
+
+namespace sf_gemv {
+
+// Batch 3..8, fp16 activations, group size 64 or 128 (one 8- or 16-byte-lane
+// block per group), K <= 8 waves x the largest block count.
+bool mfma_gemv_applies(int B, int K, int g, int xdt) {
+  const int lw = g % 128 == 0 ? 16 : 8;
+  const int maxb = lw == 16 ? WLoad<16>::kMaxBpw : WLoad<8>::kMaxBpw;
+  return xdt == SF_F16 && B >= 3 && B <= 8 && (g == 64 || g == 128) &&
+         K / (8 * lw) <= kMaxWaves * maxb;
+}
+
+// Waves per workgroup: enough that the grid holds about 3072 waves (three per
+// SIMD: all of the matrix in flight at once), at most 8, and at least enough
+// that no wave takes more than the largest block count. Blocks per wave: the
+// smallest compiled count that covers the share, so only the last wave has a
+// remainder.
+template <int LW>
+static void launch_lw(const GemvArgs &a) {
+  const int nblk = a.K / (8 * LW);
+  const int grid = (a.N + kTileN - 1) / kTileN;
+  int nw = 3072 / grid;
+  nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
+  int need = (nblk + nw - 1) / nw;
+  if (need > WLoad<LW>::kMaxBpw) need = (nblk + kMaxWaves - 1) / kMaxWaves;
+  int bpw = kBucket<LW>[5];
+  for (int b : kBucket<LW>)
+    if (b >= need) { bpw = b; break; }
+  nw = (nblk + bpw - 1) / bpw;  // every launched wave has blocks
+  if (a.asym) launch_bpw<LW, true>(a, grid, nw, nblk, bpw);
+  else launch_bpw<LW, false>(a, grid, nw, nblk, bpw);
+}
+
+int launch_mfma_gemv(const GemvArgs &a, int g) {
+  if (g % 128 == 0) launch_lw<16>(a);
+  else launch_lw<8>(a);
+  return SF_OK;
+}
+
+}  // namespace sf_gemv

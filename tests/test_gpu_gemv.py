@@ -221,3 +221,29 @@ def test_unit_vector_activations_pin_row_and_k_mapping(dev, xdtype, N, K, g):
         y = w.matmul(torch.as_tensor(X).to(dev).to(xdtype), out_dtype=torch.float32).cpu().numpy()
         exp = (q[:, kk].astype(np.float64) * s[:, np.array(kk) // g]).T
         np.testing.assert_array_equal(y, exp.astype(np.float32))
+
+
+@pytest.mark.parametrize("N,K,g,asym", [
+    (13, 64, 64, False),       # one 64-k block, rows far below a 16-row tile
+    (1000, 896, 64, True),     # 14 blocks over 7 waves, ragged last tile
+    (77, 4864, 64, False),     # 76 blocks: 7 waves of 12 (the last one shorter)
+    (4100, 11008, 128, True),  # 86 blocks of 128 k: 8 waves of 12, the last of 2
+    (64, 12288, 128, False),   # largest K on 16-byte lanes (8 waves x 12 blocks)
+    (48, 12288, 64, True),     # largest K on 8-byte lanes (8 waves x 24 blocks)
+    (40, 2048, 256, False),    # groups of 256 take the VALU kernel
+])
+def test_batch3to8_shapes(dev, N, K, g, asym):
+    """Batch 3..8 with fp16 activations and groups of 64 or 128 run on MFMA:
+    ragged row tiles, uneven K splits over waves, both load widths."""
+    rng = np.random.default_rng(N + K)
+    W = rng.normal(0.01 if asym else 0, 0.02, (N, K)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, g)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, g), None
+    x = rng.normal(0, 1, (8, K)).astype(np.float16)
+    for B in (3, 4, 5, 6, 7, 8):
+        y32, y, xk = run_gemv(dev, pk, s, z, x[:B], g)
+        ref = linear.gemv(pk, s16(s), xk.astype(np.float64), g, zeros=z)
+        linear.assert_close(y32, ref, TOL, f"N={N} K={K} g={g} asym={asym} B={B}")
+        linear.assert_close(y, ref, TOL, f"fp16 out N={N} K={K} B={B}")
