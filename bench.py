@@ -301,7 +301,7 @@ def e2e_decode(dev, runs: int = 3):
         order = sorted(range(runs), key=lambda i: rs[i].decode_tok_s)
         med = rs[order[runs // 2]]
         timer = Timer(torch, torch.cuda.Stream(dev))
-        head_us = timer.per_call_us([lambda: m._lm_head(m.xn, m.token, None, logits=False)] * 32)
+        head_us = timer.per_call_us([lambda: m._lm_head_norm(m.h, m.token, None, logits=False)] * 32)
         w_bytes = sum(getattr(L, n).nbytes for L in m.layers for n in ("qkv", "o", "gate_up", "down"))
         head_bytes = m.embed.numel() * 2
         T_mean = E2E_PROMPT + E2E_TOKENS / 2
@@ -322,7 +322,9 @@ def e2e_decode(dev, runs: int = 3):
         }
         del m
         torch.cuda.empty_cache()
-    out["launches_per_token"] = 2 + 9 * cfg.num_hidden_layers + 1
+    # embed; per layer qkv (norm folded), rope+append, attention, o, gate_up
+    # (norm folded), down (SwiGLU folded); lm_head (final norm folded)
+    out["launches_per_token"] = 1 + 6 * cfg.num_hidden_layers + 1
     return out
 
 
@@ -538,12 +540,12 @@ def main() -> int:
         profile_kernels(dev)
         return 0
     if args.profile_e2e:
-        _, m, ids = e2e_model(dev, torch.float32)
+        _, m, ids = e2e_model(dev, torch.float16)
         m.prefill(ids)
         for _ in range(8):
             m.decode_step()
         torch.cuda.synchronize()
-        print(json.dumps({"profile_e2e": "prefill 512 + 8 eager decode steps, fp32 activations"}))
+        print(json.dumps({"profile_e2e": "prefill 512 + 8 eager decode steps, fp16 activations"}))
         return 0
 
     sweep = GpuSweep(dev)

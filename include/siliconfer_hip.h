@@ -84,6 +84,23 @@ int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtyp
                const void *bias, int bias_dtype, int B, int N, int K, int group_size,
                int has_zeros, void *stream);
 
+/* The decode GEMV (batch 1) with the operation that produces its input folded
+ * into the activation load, for the decoder step (no counterpart in the
+ * reference, which runs RMSNorm / SwiGLU and the Q4Linear as separate ops:
+ * /root/reference/siliconfer/model/layers.py:14-21, 143-144):
+ *   op SF_PRE_RMSNORM:  x = src[0:K] * rsqrt(mean(src^2) + eps) * norm_w
+ *                       (src the fp32 residual row [K], norm_w fp32 [K]);
+ *   op SF_PRE_SILU_MUL: x[k] = silu(src[k]) * src[K + k]
+ *                       (src the fp32 gate|up row [2K]; norm_w unused).
+ * x is rounded to act_dtype (SF_F16 / SF_BF16 / SF_F32) before the product,
+ * and the result is bit-identical to sf_rmsnorm / sf_silu_mul writing an
+ * act_dtype buffer followed by sf_q4_gemv on it. Outputs as sf_q4_gemv. */
+#define SF_PRE_RMSNORM 1
+#define SF_PRE_SILU_MUL 2
+int sf_q4_gemv_fused(const void *blob, const float *src, int op, const float *norm_w, float eps,
+                     int act_dtype, void *y, int y_dtype, float *y_f32, const void *bias,
+                     int bias_dtype, int N, int K, int group_size, int has_zeros, void *stream);
+
 /* ---- prefill GEMM (M rows) ------------------------------------------------
  * Y[m, n] = X[m, :] . dequant(W)[n, :] for M rows; replaces q4_gemm_sym /
  * q4_gemm_asym (bindings.cpp:98-150; q4_gemm.cpp:12-51). bf16/f16 MFMA on
@@ -193,6 +210,15 @@ size_t sf_lm_head_workspace_bytes(int V);
 int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, float *logits, int V, int H,
                       int32_t *token_out, int *pos_inc, int32_t *hist, void *workspace,
                       size_t workspace_bytes, void *stream);
+
+/* sf_lm_head_argmax with the final RMSNorm (llama.py:76) folded in: x =
+ * h * rsqrt(mean(h^2) + eps) * norm_w for the fp32 residual row h [H], rounded
+ * to act_dtype; bit-identical to sf_rmsnorm into an act_dtype buffer followed
+ * by sf_lm_head_argmax on it. */
+int sf_lm_head_argmax_rmsnorm(const void *w, const float *h, const float *norm_w, float eps,
+                              int act_dtype, float *logits, int V, int H, int32_t *token_out,
+                              int *pos_inc, int32_t *hist, void *workspace, size_t workspace_bytes,
+                              void *stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsiliconfer_hip.so")
 
 SF_F32, SF_F16, SF_BF16 = 0, 1, 2
+SF_PRE_RMSNORM, SF_PRE_SILU_MUL = 1, 2
 _DT = {torch.float32: SF_F32, torch.float16: SF_F16, torch.bfloat16: SF_BF16}
 
 _c_i, _c_f, _c_sz, _c_p = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
@@ -34,6 +35,8 @@ _SIGS = {
     "sf_q4_unpack": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "sf_q4_gemv": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
+    "sf_q4_gemv_fused": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_f, _c_i, _c_p, _c_i, _c_p, _c_p,
+                                _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_q4_gemm_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
     "sf_q4_gemm": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),
@@ -57,6 +60,8 @@ _SIGS = {
     "sf_lm_head_workspace_bytes": (_c_sz, [_c_i]),
     "sf_lm_head_argmax": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p,
                                  _c_sz, _c_p]),
+    "sf_lm_head_argmax_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_f, _c_i, _c_p, _c_i, _c_i, _c_p,
+                                         _c_p, _c_p, _c_p, _c_sz, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -24,6 +24,7 @@
 //    launch with the reference's combine rule (q4_attention.py:63-70,
 //    256-261); a single split writes the output directly.
 #include <math.h>
+#include <stdlib.h>
 
 #include "sf_common.h"
 
@@ -164,6 +165,141 @@ constexpr int attn_smem_floats() {
   constexpr int a = 2048 * HB + 2 * 256 * HB + 2 * HB;
   constexpr int b = 4 * kAttnThreads + 2 * HB * kMaxSplits + HB;
   return a > b ? a : b;
+}
+
+// Cross-split merge of a split-T launch, called by every workgroup after it
+// has stored its partial (m, l, acc[D] per head) with agent-scope stores: the
+// last workgroup of the (b, kv head, head block) group to arrive (counter
+// `ctr`) merges all splits' partials with the reference's combine rule
+// (q4_attention.py:63-70, 256-261), writes the output rows bh0 .. bh0+nh-1
+// and resets the counter. smem holds at least 4 * kAttnThreads + 2 * HB *
+// MAXS + HB floats.
+template <int HB, int MAXS>
+__device__ __forceinline__ void attn_merge_splits(float *smem, int *s_last, const float *part_acc,
+                                                  const float *part_ml, unsigned *ctr, size_t bh0,
+                                                  int nh, int D, int n_splits, void *out, int odt) {
+  constexpr int NT = kAttnThreads;
+  const int tid = threadIdx.x;
+  const int nq = D >> 2;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = prev == (unsigned)(n_splits - 1);
+  }
+  __syncthreads();
+  if (!*s_last) return;
+
+  // Partials of (head, 4-dim quad) items; with fewer items than threads the
+  // splits are cut into nsl slices whose sums are folded through LDS. Each
+  // thread's first kMergeChunk partials are loaded before the (m, l) staging
+  // so that all loads of the merge are in flight together.
+  float4_t *red4 = (float4_t *)smem;        // [NT]
+  float *cw = smem + 4 * NT;                // [HB][MAXS]: m, then weights
+  float *cl = cw + HB * MAXS;         // [HB][MAXS]: l
+  float *Lg = cl + HB * MAXS;         // [HB]
+  const int items = nh * nq;
+  const int nsl = items >= NT ? 1 : NT / items;
+  const int units = items * nsl;            // (item, slice) pairs
+  auto part4 = [&](int item, int s) {
+    const int h = item / nq, dqq = (item - h * nq) * 4;
+    const float *pp = part_acc + ((bh0 + h) * n_splits + s) * D + dqq;
+    const float2_t lo = ld2_agent(pp), hi = ld2_agent(pp + 2);
+    return float4_t{lo.x, lo.y, hi.x, hi.y};
+  };
+  constexpr int CH = kMergeChunk;
+  float4_t pre[CH];
+  {
+    const int unit = tid < units ? tid : 0;
+    const int item = unit % items, sl = unit / items;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) pre[j] = part4(item, min(sl + j * nsl, n_splits - 1));
+  }
+  // split weights: 32 lanes per head, lane j covering splits j, j + 32, ...;
+  // heads h0 + tid / 32 for h0 = 0, 8, ... (every thread takes the same number
+  // of rounds, so the 32-lane reductions always see whole groups)
+  for (int h0 = 0; h0 < HB; h0 += NT / 32) {
+    const int h = h0 + (tid >> 5), j = tid & 31;
+    const bool on = h < nh;
+    const float *mlh = part_ml + (bh0 + (on ? h : 0)) * n_splits * 2;
+    // the first two are loaded unconditionally (clamped) to keep them in flight together
+    const float2_t ml0 = ld2_agent(mlh + 2 * min(j, n_splits - 1));
+    const float2_t ml1 = ld2_agent(mlh + 2 * min(j + 32, n_splits - 1));
+    float mx = -INFINITY;
+    if (on) {
+      if (j < n_splits) {
+        cw[h * MAXS + j] = ml0.x;
+        cl[h * MAXS + j] = ml0.y;
+        mx = ml0.x;
+      }
+      if (j + 32 < n_splits) {
+        cw[h * MAXS + j + 32] = ml1.x;
+        cl[h * MAXS + j + 32] = ml1.y;
+        mx = fmaxf(mx, ml1.x);
+      }
+      for (int s = j + 64; s < n_splits; s += 32) {
+        const float2_t ml = ld2_agent(mlh + 2 * s);
+        cw[h * MAXS + s] = ml.x;
+        cl[h * MAXS + s] = ml.y;
+        mx = fmaxf(mx, ml.x);
+      }
+    }
+    const float M = group32_max(mx);
+    const float M_ref = M == -INFINITY ? 0.f : M;
+    float lsum = 0.f;
+    if (on)
+      for (int s = j; s < n_splits; s += 32) {
+        const float w = __builtin_amdgcn_exp2f(cw[h * MAXS + s] - M_ref);
+        cw[h * MAXS + s] = w;
+        lsum = fmaf(cl[h * MAXS + s], w, lsum);
+      }
+    lsum = group32_sum(lsum);
+    if (on && j == 0) Lg[h] = lsum;
+  }
+  __syncthreads();
+  auto unit_sum = [&](int unit, bool first) {
+    const int item = unit % items, sl = unit / items, h = item / nq;
+    const float *w = cw + h * MAXS;
+    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    int j0 = 0;
+    if (first) {
+#pragma unroll
+      for (int j = 0; j < CH; j += 2) {
+        const int s0 = sl + j * nsl, s1 = s0 + nsl;
+        a0 += pre[j] * (s0 < n_splits ? w[s0] : 0.f);
+        a1 += pre[j + 1] * (s1 < n_splits ? w[s1] : 0.f);
+      }
+      j0 = CH;
+    }
+    for (int s = sl + j0 * nsl; s < n_splits; s += nsl) a0 += part4(item, s) * w[s];
+    return a0 + a1;
+  };
+  auto write_item = [&](int item, float4_t a) {
+    const int h = item / nq, dqq = (item - h * nq) * 4;
+    const float L = Lg[h];
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const size_t o = (bh0 + h) * D + dqq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = a[i] * inv;
+      if (odt == SF_F32) ((float *)out)[o + i] = v;
+      else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
+      else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
+    }
+  };
+  if (nsl == 1) {
+    for (int item = tid; item < items; item += NT) write_item(item, unit_sum(item, item == tid));
+  } else {
+    if (tid < units) red4[tid] = unit_sum(tid, true);
+    __syncthreads();
+    if (tid < items) {
+      float4_t a = red4[tid];
+      for (int k = 1; k < nsl; ++k) a += red4[k * items + tid];
+      write_item(tid, a);
+    }
+  }
+  if (tid == 0)  // ready for the next call on this workspace
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One workgroup per (split, kv head, block of HB query heads, batch row); the
@@ -401,125 +537,270 @@ k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
     st_agent(part_ml + ((bh0 + tid) * n_splits + split) * 2 + 1, Ls[tid]);
   }
 
-  // ---- the last split of this (b, kv head, head block) merges all partials
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
-  unsigned *ctr = counters + ((size_t)b * KVH + kvh) * n_hblk + hblk;
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(n_splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
+  attn_merge_splits<HB, kMaxSplits>(smem, &s_last, part_acc, part_ml,
+                                     counters + ((size_t)b * KVH + kvh) * n_hblk + hblk, bh0, nh, D,
+                                     n_splits, out, odt);
+}
 
-  // Partials of (head, 4-dim quad) items; with fewer items than threads the
-  // splits are cut into nsl slices whose sums are folded through LDS. Each
-  // thread's first kMergeChunk partials are loaded before the (m, l) staging
-  // so that all loads of the merge are in flight together.
-  float4_t *red4 = (float4_t *)smem;        // [NT]
-  float *cw = smem + 4 * NT;                // [HB][kMaxSplits]: m, then weights
-  float *cl = cw + HB * kMaxSplits;         // [HB][kMaxSplits]: l
-  float *Lg = cl + HB * kMaxSplits;         // [HB]
-  const int items = nh * nq;
-  const int nsl = items >= NT ? 1 : NT / items;
-  const int units = items * nsl;            // (item, slice) pairs
-  auto part4 = [&](int item, int s) {
-    const int h = item / nq, dqq = (item - h * nq) * 4;
-    const float *pp = part_acc + ((bh0 + h) * n_splits + s) * D + dqq;
-    const float2_t lo = ld2_agent(pp), hi = ld2_agent(pp + 2);
-    return float4_t{lo.x, lo.y, hi.x, hi.y};
-  };
-  constexpr int CH = kMergeChunk;
-  float4_t pre[CH];
-  {
-    const int unit = tid < units ? tid : 0;
-    const int item = unit % items, sl = unit / items;
+// ---------------------------------------------------------------------------
+// MFMA decode attention: G <= 16 query heads per kv head, D = 64 or 128
+// ---------------------------------------------------------------------------
+// Per wave, 32-token tiles of one split (tile j of the split goes to wave
+// j % 4). q . K^T and P V run as v_mfma_f32_16x16x32_f16 with the heads on the
+// 16-wide N side (rows >= G are zero queries whose outputs are dropped):
+//  * S^T = K q^T: A = the K codes of 16 tokens (lane l: token l % 16, dims
+//    D/4 (l / 16) + 8 ks .. + 7 of k-step ks; int8 -> fp16 is exact), B = q
+//    (fp16; fp32 / bf16 queries as an fp16 hi + lo pair, two MFMAs). C holds
+//    tokens 4 (l / 16) + i, head l % 16 — for the two 16-token halves of the
+//    tile, the 8 tokens T_g = {4g .. 4g+3, 16+4g .. 16+4g+3}, g = l / 16.
+//  * Scores are scaled (k scale x softmax scale x log2 e) and masked, and each
+//    head keeps a base-2 online softmax; a head's max is taken over its 4
+//    lanes (shuffles) so that m is the same in all of them.
+//  * O^T = V^T P^T: B = P^T needs exactly the 8 tokens T_g in lane l, which
+//    the QK output already holds (the V scale folded into P, fp16 hi + lo);
+//    A = V^T: the wave stages the tile's V codes in LDS (row pitch D + 8
+//    bytes, which keeps the reads below free of bank conflicts) and reads 8
+//    tokens of one dim per lane with ds_read_b64_tr_b8: within each 16-lane
+//    group, lane i < 8 receives byte i of the rows that the even lanes
+//    address and lane 8 + i byte i of the odd lanes' rows, so lane 2s + h of
+//    group g addresses token T_g[s], dims 16 db + 8 h .. + 7.
+// The next tile's loads are issued before the current tile's math. At the
+// end the 4 wave states are merged through LDS into the split's partial (or
+// the output), then attn_merge_splits combines the splits.
+constexpr int kMfmaMaxSplits = 128;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+// 8 int8 codes (two dwords, byte order kept) -> 8 exact fp16 values: the
+// offset-binary byte b + 128 in the low mantissa byte of fp16 1024, minus 1152.
+__device__ __forceinline__ half8_t i8x8_to_h8(uint32_t lo, uint32_t hi) {
+  const uint32_t a = lo ^ 0x80808080u, b = hi ^ 0x80808080u;
+  const half2_t off = {(f16)-1152.f, (f16)-1152.f};
+  const half2_t p0 = sf_bitcast<half2_t>(__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) + off;
+  const half2_t p1 = sf_bitcast<half2_t>(__builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) + off;
+  const half2_t p2 = sf_bitcast<half2_t>(__builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) + off;
+  const half2_t p3 = sf_bitcast<half2_t>(__builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) + off;
+  return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <int D>
+constexpr int attn_mfma_smem_floats() {
+  // main phase: V tiles [4][32][D + 8] bytes, then wave states m, l [4][16]
+  // and O [4][16][D]; merge phase: attn_merge_splits<16, kMfmaMaxSplits>
+  constexpr int a = kAttnWaves * 32 * (D + 8) / 4 + 2 * kAttnWaves * 16 + kAttnWaves * 16 * D;
+  constexpr int b = 4 * kAttnThreads + 2 * 16 * kMfmaMaxSplits + 16;
+  return a > b ? a : b;
+}
+
+template <int QDT, int SDT, int D>
+__global__ void __launch_bounds__(kAttnThreads)
+k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
+            const int8_t *__restrict__ vc, const void *__restrict__ vs, float *part_acc,
+            float *part_ml, unsigned *counters, void *__restrict__ out, int odt, int H, int KVH,
+            int T, const int *__restrict__ T_dev, int causal, int T_cap, float qscale,
+            int n_splits) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int NW = kAttnWaves;
+  constexpr int KS = D / 32;       // q.k k-steps per token
+  constexpr int DB = D / 16;       // P V dim blocks
+  constexpr int KW = D / 16;       // K dwords per lane per token (D/4 bytes)
+  constexpr int VC = D / 32;       // 16-byte V chunks per lane per tile
+  constexpr int PITCH = D + 8;     // V tile row pitch in LDS, bytes
+  constexpr bool QSPLIT = QDT != SF_F16;
+  __shared__ __attribute__((aligned(16))) float smem[attn_mfma_smem_floats<D>()];
+  __shared__ int s_last;
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = H / KVH;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int hl = lane & 15, g = lane >> 4;
+  int Tv = T_dev ? *T_dev + T : T;
+  if (causal) Tv = T + b + 1;
+  Tv = max(0, min(Tv, T_cap));
+  const int tile = (Tv + n_splits - 1) / n_splits;
+  const int t0 = split * tile, t1 = min(t0 + tile, Tv);
+  const size_t base = ((size_t)(causal ? 0 : b) * KVH + kvh) * (size_t)T_cap;
+  const size_t bh0 = (size_t)b * H + (size_t)kvh * G;
+
+  // q as the B operand of S^T = K q^T: lane (head hl, group g), k-step ks:
+  // q[hl][D/4 g + 8 ks .. + 7]
+  half8_t qh[KS], ql[KS];
 #pragma unroll
-    for (int j = 0; j < CH; ++j) pre[j] = part4(item, min(sl + j * nsl, n_splits - 1));
+  for (int k = 0; k < KS; ++k) {
+    float f[8];
+    sf_load8_as_f32<QDT>(q, (bh0 + min(hl, G - 1)) * D + g * (D / 4) + 8 * k, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = hl < G ? f[i] : 0.f;
+      qh[k][i] = (f16)v;
+      ql[k][i] = (f16)(v - (float)qh[k][i]);
+    }
   }
-  // split weights: 32 lanes per head, lane j covering splits j, j + 32, ...
-  {
-    const int h = tid >> 5, j = tid & 31;
-    const bool on = h < nh;
-    const float *mlh = part_ml + (bh0 + (on ? h : 0)) * n_splits * 2;
-    // the first two are loaded unconditionally (clamped) to keep them in flight together
-    const float2_t ml0 = ld2_agent(mlh + 2 * min(j, n_splits - 1));
-    const float2_t ml1 = ld2_agent(mlh + 2 * min(j + 32, n_splits - 1));
+
+  struct Tile {
+    u32x4 k[2][KW / 4];  // K dwords of tokens hl and 16 + hl
+    u32x4 v[VC];         // V chunks for the LDS stage
+    float ks[8], vs[8];  // scales of the lane's tokens T_g
+  };
+  const int ntiles = t1 > t0 ? (t1 - t0 + 31) / 32 : 0;
+  auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
+  auto load = [&](int j, Tile &tl) {
+    const int tb = t0 + 32 * j;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int t = min(tb + 16 * h2 + hl, t1 - 1);
+      const u32x4 *kp = (const u32x4 *)(kc + (base + t) * D + g * (D / 4));
+#pragma unroll
+      for (int c = 0; c < KW / 4; ++c) tl.k[h2][c] = kp[c];
+    }
+#pragma unroll
+    for (int c = 0; c < VC; ++c) {
+      const int ch = lane + 64 * c, tok = ch / (D / 16), piece = ch % (D / 16);
+      const int t = min(tb + tok, t1 - 1);
+      tl.v[c] = *(const u32x4 *)(vc + (base + t) * D + piece * 16);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const size_t row = base + min(tb + tok_of(r), t1 - 1);
+      tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
+      tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
+    }
+  };
+
+  uint8_t *vt = (uint8_t *)smem + wave * 32 * PITCH;
+  float m = -INFINITY, lsum = 0.f;
+  float4_t O[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) O[d] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int j, const Tile &tl) {
+    const int tb = t0 + 32 * j;
+    // S^T for the two 16-token halves
+    float4_t S[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      S[h2] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const u32x4 w = tl.k[h2][k / 2];
+        const half8_t a = (k & 1) ? i8x8_to_h8(w.z, w.w) : i8x8_to_h8(w.x, w.y);
+        S[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[k], S[h2], 0, 0, 0);
+        if constexpr (QSPLIT) S[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[k], S[h2], 0, 0, 0);
+      }
+    }
+    float sc[8];
     float mx = -INFINITY;
-    if (on) {
-      if (j < n_splits) {
-        cw[h * kMaxSplits + j] = ml0.x;
-        cl[h * kMaxSplits + j] = ml0.y;
-        mx = ml0.x;
-      }
-      if (j + 32 < n_splits) {
-        cw[h * kMaxSplits + j + 32] = ml1.x;
-        cl[h * kMaxSplits + j + 32] = ml1.y;
-        mx = fmaxf(mx, ml1.x);
-      }
-      for (int s = j + 64; s < n_splits; s += 32) {
-        const float2_t ml = ld2_agent(mlh + 2 * s);
-        cw[h * kMaxSplits + s] = ml.x;
-        cl[h * kMaxSplits + s] = ml.y;
-        mx = fmaxf(mx, ml.x);
-      }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const bool valid = tb + tok_of(r) < t1;
+      sc[r] = valid ? S[r >> 2][r & 3] * (tl.ks[r] * qscale) : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
     }
-    const float M = group32_max(mx);
-    const float M_ref = M == -INFINITY ? 0.f : M;
-    float lsum = 0.f;
-    if (on)
-      for (int s = j; s < n_splits; s += 32) {
-        const float w = __builtin_amdgcn_exp2f(cw[h * kMaxSplits + s] - M_ref);
-        cw[h * kMaxSplits + s] = w;
-        lsum = fmaf(cl[h * kMaxSplits + s], w, lsum);
-      }
-    lsum = group32_sum(lsum);
-    if (on && j == 0) Lg[h] = lsum;
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float c = __builtin_amdgcn_exp2f(m - m_ref);  // exp2(-inf) = 0
+    m = m_new;
+    half8_t ph, pl;
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
+      ps += p;
+      const float pv = p * tl.vs[r];
+      ph[r] = (f16)pv;
+      pl[r] = (f16)(pv - (float)ph[r]);
+    }
+    lsum = fmaf(lsum, c, ps);
+    // V tile -> LDS (this wave's region; LDS accesses of a wave stay in order)
+#pragma unroll
+    for (int cc = 0; cc < VC; ++cc) {
+      const int ch = lane + 64 * cc, tok = ch / (D / 16), piece = ch % (D / 16);
+      uint2 *dst = (uint2 *)(vt + tok * PITCH + piece * 16);
+      dst[0] = uint2{tl.v[cc].x, tl.v[cc].y};
+      dst[1] = uint2{tl.v[cc].z, tl.v[cc].w};
+    }
+    const int vtok = tok_of(hl >> 1);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      typedef int v2i __attribute__((ext_vector_type(2)));
+      const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i *)(vt + vtok * PITCH + 16 * d + 8 * (hl & 1)));
+      const half8_t a = i8x8_to_h8((uint32_t)r.x, (uint32_t)r.y);
+      O[d] *= c;
+      O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, O[d], 0, 0, 0);
+      O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, O[d], 0, 0, 0);
+    }
+  };
+
+  if (wave < ntiles) {
+    Tile b0, b1;
+    load(wave, b0);
+    for (int j = wave; j < ntiles; j += 2 * NW) {
+      if (j + NW < ntiles) load(j + NW, b1);
+      compute(j, b0);
+      if (j + NW >= ntiles) break;
+      if (j + 2 * NW < ntiles) load(j + 2 * NW, b0);
+      compute(j + NW, b1);
+    }
   }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+
+  // ---- merge the 4 wave states (LDS)
+  float *ms = smem + NW * 32 * PITCH / 4;  // [NW][16]
+  float *ls = ms + NW * 16;                // [NW][16]
+  float *os = ls + NW * 16;                // [NW][16][D]
+  if (g == 0) {
+    ms[wave * 16 + hl] = m;
+    ls[wave * 16 + hl] = lsum;
+  }
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) os[(wave * 16 + hl) * D + 16 * d + 4 * g + i] = O[d][i];
   __syncthreads();
-  auto unit_sum = [&](int unit, bool first) {
-    const int item = unit % items, sl = unit / items, h = item / nq;
-    const float *w = cw + h * kMaxSplits;
-    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-    int j0 = 0;
-    if (first) {
+  const bool single = n_splits == 1;
+  constexpr int NQ = D / 4;
+  for (int it = tid; it < G * NQ; it += kAttnThreads) {
+    const int h = it / NQ, d4 = (it - h * NQ) * 4;
+    float M = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < CH; j += 2) {
-        const int s0 = sl + j * nsl, s1 = s0 + nsl;
-        a0 += pre[j] * (s0 < n_splits ? w[s0] : 0.f);
-        a1 += pre[j + 1] * (s1 < n_splits ? w[s1] : 0.f);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, ms[w * 16 + h]);
+    const float M_ref = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(ms[w * 16 + h] - M_ref);
+      L = fmaf(wt, ls[w * 16 + h], L);
+      a += *(const float4_t *)(os + (w * 16 + h) * D + d4) * wt;
+    }
+    if (single) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const size_t o = (bh0 + h) * D + d4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = a[i] * inv;
+        if (odt == SF_F32) ((float *)out)[o + i] = v;
+        else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
+        else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
       }
-      j0 = CH;
-    }
-    for (int s = sl + j0 * nsl; s < n_splits; s += nsl) a0 += part4(item, s) * w[s];
-    return a0 + a1;
-  };
-  auto write_item = [&](int item, float4_t a) {
-    const int h = item / nq, dqq = (item - h * nq) * 4;
-    const float L = Lg[h];
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const size_t o = (bh0 + h) * D + dqq;
+    } else {
+      float *pa = part_acc + ((bh0 + h) * n_splits + split) * D + d4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = a[i] * inv;
-      if (odt == SF_F32) ((float *)out)[o + i] = v;
-      else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
-      else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
-    }
-  };
-  if (nsl == 1) {
-    for (int item = tid; item < items; item += NT) write_item(item, unit_sum(item, item == tid));
-  } else {
-    if (tid < units) red4[tid] = unit_sum(tid, true);
-    __syncthreads();
-    if (tid < items) {
-      float4_t a = red4[tid];
-      for (int k = 1; k < nsl; ++k) a += red4[k * items + tid];
-      write_item(tid, a);
+      for (int i = 0; i < 4; ++i) st_agent(pa + i, a[i]);
+      if (d4 == 0) {
+        st_agent(part_ml + ((bh0 + h) * n_splits + split) * 2 + 0, M);
+        st_agent(part_ml + ((bh0 + h) * n_splits + split) * 2 + 1, L);
+      }
     }
   }
-  if (tid == 0)  // ready for the next call on this workspace
-    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (single) return;
+  attn_merge_splits<16, kMfmaMaxSplits>(smem, &s_last, part_acc, part_ml,
+                                        counters + (size_t)b * KVH + kvh, bh0, G, D, n_splits,
+                                        out, odt);
 }
 
 int pow2_log2_at_least(int v) {
@@ -648,15 +929,48 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
     counters = (unsigned *)workspace;
   }
   const int G = H / KVH;
+  const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
+  hipStream_t st = (hipStream_t)stream;
+  // MFMA kernel: up to 16 query heads per kv head, head_dim 64 or 128,
+  // 16-byte aligned codes (SF_ATTN_MFMA=0 keeps the VALU kernel)
+  const char *mfma_env = getenv("SF_ATTN_MFMA");
+  const bool mfma_ok = !(mfma_env && mfma_env[0] == '0');
+  if (mfma_ok && G <= 16 && (D == 64 || D == 128) && n_splits <= kMfmaMaxSplits &&
+      (((uintptr_t)k_codes | (uintptr_t)v_codes) & 15) == 0) {
+    SF_REQUIRE(n_splits == 1 || B * KVH <= kMaxCounters, SF_EUNSUPPORTED,
+               "attention batch too large for one call (B * n_kv_heads = %d > %d)", B * KVH,
+               kMaxCounters);
+    dim3 grid(n_splits, KVH, B);
+#define SF_MFMA_LAUNCH(QD, SD, DD)                                                              \
+  k_attn_mfma<QD, SD, DD><<<grid, kAttnThreads, 0, st>>>(q, k_codes, k_scales, v_codes, v_scales, \
+                                                         part_acc, part_ml, counters, out,       \
+                                                         out_dtype, H, KVH, T, T_dev, causal,    \
+                                                         T_cap, qscale, n_splits)
+#define SF_MFMA_D(QD, SD)                     \
+  do {                                        \
+    if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64);  \
+    else SF_MFMA_LAUNCH(QD, SD, 128);         \
+  } while (0)
+    if (scale_dtype == SF_F16) {
+      if (q_dtype == SF_F32) SF_MFMA_D(SF_F32, SF_F16);
+      else if (q_dtype == SF_F16) SF_MFMA_D(SF_F16, SF_F16);
+      else SF_MFMA_D(SF_BF16, SF_F16);
+    } else {
+      if (q_dtype == SF_F32) SF_MFMA_D(SF_F32, SF_F32);
+      else if (q_dtype == SF_F16) SF_MFMA_D(SF_F16, SF_F32);
+      else SF_MFMA_D(SF_BF16, SF_F32);
+    }
+#undef SF_MFMA_D
+#undef SF_MFMA_LAUNCH
+    return sf_check_launch(what);
+  }
   const int HB = attn_heads_per_block(G);
   const int n_hblk = (G + HB - 1) / HB;
   SF_REQUIRE(n_splits == 1 || B * KVH * n_hblk <= kMaxCounters, SF_EUNSUPPORTED,
              "attention batch too large for one call (B * n_kv_heads * head blocks = %d > %d)",
              B * KVH * n_hblk, kMaxCounters);
   const int oct_log2 = pow2_log2_at_least(D / 8);
-  const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
   dim3 grid(n_splits, KVH * n_hblk, B);
-  hipStream_t st = (hipStream_t)stream;
 #define SF_ATTN_LAUNCH(QD, SD, HBV)                                                            \
   k_attn_decode<QD, SD, HBV><<<grid, kAttnThreads, 0, st>>>(                                   \
       q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H, \

@@ -23,37 +23,9 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f<0x141>(v);  // row_half_mirror
-  v += dpp_f<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
-}
-
-// Sum over the block (blockDim.x a multiple of 64, at most 1024); every
-// thread gets the result. `red` holds one float per wave.
-__device__ __forceinline__ float block_sum(float v, float *red) {
-  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int w = 0; w < nw; ++w) t += red[w];
-  return t;
 }
 
 __device__ __forceinline__ void store_as(void *p, int dt, size_t i, float v) {
@@ -81,25 +53,22 @@ k_embed(const int32_t *__restrict__ ids, const void *__restrict__ table, int tdt
 
 // ---------------------------------------------------------------------------
 // One block per row. mx.fast.rms_norm semantics: fp32 mean of squares,
-// x * rsqrt(mean + eps) * w.
+// x * rsqrt(mean + eps) * w. Every wave computes the row's norm itself with
+// sf_row_inv_rms (the order the projections that fold the norm in use too).
 __global__ void __launch_bounds__(kThreads)
 k_rmsnorm(float *__restrict__ x, const float *__restrict__ delta, const void *__restrict__ w,
           int wdt, void *__restrict__ out, int odt, int H, float eps) {
-  __shared__ float red[kThreads / 64];
   const size_t r0 = (size_t)blockIdx.x * H;
-  float ss = 0.f;
+  const float inv = sf_row_inv_rms(x + r0, delta ? delta + r0 : nullptr, H, eps);
+  if (delta) __syncthreads();  // every wave has read x before it is overwritten
   for (int h = threadIdx.x; h < H; h += blockDim.x) {
     float v = x[r0 + h];
     if (delta) {
       v += delta[r0 + h];
       x[r0 + h] = v;
     }
-    ss = fmaf(v, v, ss);
+    store_as(out, odt, r0 + h, sf_opaque(v * inv * load_as(w, wdt, h)));
   }
-  ss = block_sum(ss, red);
-  const float inv = 1.f / sqrtf(ss / (float)H + eps);
-  for (int h = threadIdx.x; h < H; h += blockDim.x)
-    store_as(out, odt, r0 + h, x[r0 + h] * inv * load_as(w, wdt, h));
 }
 
 // ---------------------------------------------------------------------------
@@ -184,7 +153,7 @@ k_silu_mul(const float *__restrict__ gu, void *__restrict__ out, int odt, int I,
        t += (long long)gridDim.x * blockDim.x) {
     const long long r = t / I, i = t - r * I;
     const float g = gu[r * 2 * I + i], u = gu[r * 2 * I + I + i];
-    store_as(out, odt, (size_t)t, g / (1.f + expf(-g)) * u);
+    store_as(out, odt, (size_t)t, sf_silu_mul(g, u));
   }
 }
 
@@ -204,18 +173,27 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-template <int XDT>
+// NORM: x is the fp32 residual row and the block applies the final RMSNorm
+// itself (sf_row_inv_rms, then x * inv * norm_w rounded to XDT, the values
+// sf_rmsnorm would have stored in an XDT buffer).
+template <int XDT, bool NORM>
 __global__ void __launch_bounds__(kThreads)
 k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
-                 float *__restrict__ logits, int V, int H, int32_t *__restrict__ token_out,
-                 int *__restrict__ pos_inc, int32_t *__restrict__ hist, float *part_val,
-                 int *part_idx, unsigned *counter) {
+                 const float *__restrict__ norm_w, float eps, float *__restrict__ logits, int V,
+                 int H, int32_t *__restrict__ token_out, int *__restrict__ pos_inc,
+                 int32_t *__restrict__ hist, float *part_val, int *part_idx, unsigned *counter) {
   __shared__ __attribute__((aligned(16))) float xs[kHeadMaxH];
   __shared__ float bv_s[kThreads / 64];
   __shared__ int bi_s[kThreads / 64];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int h = tid; h < H; h += kThreads) xs[h] = sf_load_as_f32<XDT>(x, h);
+  if constexpr (NORM) {
+    const float *xf = (const float *)x;
+    const float inv = sf_row_inv_rms(xf, nullptr, H, eps);
+    for (int h = tid; h < H; h += kThreads) xs[h] = sf_round_as<XDT>(xf[h] * inv * norm_w[h]);
+  } else {
+    for (int h = tid; h < H; h += kThreads) xs[h] = sf_load_as_f32<XDT>(x, h);
+  }
   __syncthreads();
   const int nch = H >> 3;  // 16-byte chunks per row
   const int n_waves = gridDim.x * (kThreads / 64);
@@ -265,7 +243,7 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
     }
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
-      const float a = wave_sum(acc[u]);
+      const float a = sf_wave_sum(acc[u]);
       const int row = r0 + u * n_waves;
       if (row < V) {
         if (lane == 0 && logits) logits[row] = a;
@@ -424,9 +402,9 @@ extern "C" size_t sf_lm_head_workspace_bytes(int V) {
   return 256 + (size_t)kHeadBlocks * (sizeof(float) + sizeof(int));
 }
 
-extern "C" int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, float *logits, int V,
-                                 int H, int32_t *token_out, int *pos_inc, int32_t *hist,
-                                 void *workspace, size_t workspace_bytes, void *stream) {
+static int lm_head_launch(const void *w, const void *x, int x_dtype, const float *norm_w,
+                          float eps, float *logits, int V, int H, int32_t *token_out, int *pos_inc,
+                          int32_t *hist, void *workspace, size_t workspace_bytes, void *stream) {
   SF_REQUIRE(V > 0 && H > 0, SF_EINVAL, "invalid lm_head shape V=%d H=%d", V, H);
   SF_REQUIRE(H % 8 == 0 && H <= kHeadMaxH, SF_EUNSUPPORTED,
              "hidden=%d: need a multiple of 8 up to %d", H, kHeadMaxH);
@@ -443,14 +421,37 @@ extern "C" int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, floa
   int *pi = (int *)(pv + kHeadBlocks);
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *wb = (const uint16_t *)w;
-  if (x_dtype == SF_F32)
-    k_lm_head_argmax<SF_F32><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
-                                                               pos_inc, hist, pv, pi, counter);
-  else if (x_dtype == SF_F16)
-    k_lm_head_argmax<SF_F16><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
-                                                               pos_inc, hist, pv, pi, counter);
-  else
-    k_lm_head_argmax<SF_BF16><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, logits, V, H, token_out,
-                                                                pos_inc, hist, pv, pi, counter);
-  return sf_check_launch("sf_lm_head_argmax");
+#define SF_HEAD(XD, NM)                                                                        \
+  k_lm_head_argmax<XD, NM><<<kHeadBlocks, kThreads, 0, st>>>(wb, x, norm_w, eps, logits, V, H, \
+                                                             token_out, pos_inc, hist, pv, pi, \
+                                                             counter)
+  if (norm_w) {
+    if (x_dtype == SF_F32) SF_HEAD(SF_F32, true);
+    else if (x_dtype == SF_F16) SF_HEAD(SF_F16, true);
+    else SF_HEAD(SF_BF16, true);
+  } else {
+    if (x_dtype == SF_F32) SF_HEAD(SF_F32, false);
+    else if (x_dtype == SF_F16) SF_HEAD(SF_F16, false);
+    else SF_HEAD(SF_BF16, false);
+  }
+#undef SF_HEAD
+  return SF_OK;
+}
+
+extern "C" int sf_lm_head_argmax(const void *w, const void *x, int x_dtype, float *logits, int V,
+                                 int H, int32_t *token_out, int *pos_inc, int32_t *hist,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  const int rc = lm_head_launch(w, x, x_dtype, nullptr, 0.f, logits, V, H, token_out, pos_inc,
+                                hist, workspace, workspace_bytes, stream);
+  return rc ? rc : sf_check_launch("sf_lm_head_argmax");
+}
+
+extern "C" int sf_lm_head_argmax_rmsnorm(const void *w, const float *h, const float *norm_w,
+                                         float eps, int act_dtype, float *logits, int V, int H,
+                                         int32_t *token_out, int *pos_inc, int32_t *hist,
+                                         void *workspace, size_t workspace_bytes, void *stream) {
+  SF_REQUIRE(norm_w, SF_EINVAL, "null norm weight");
+  const int rc = lm_head_launch(w, h, act_dtype, norm_w, eps, logits, V, H, token_out, pos_inc,
+                                hist, workspace, workspace_bytes, stream);
+  return rc ? rc : sf_check_launch("sf_lm_head_argmax_rmsnorm");
 }

@@ -7,6 +7,9 @@ int launch_mfma_gemv(const GemvArgs &a, int g);
 extern template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_BF16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
+extern template void launch_pre<SF_F16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
+extern template void launch_pre<SF_BF16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
+extern template void launch_pre<SF_F32>(const GemvPlan &, const GemvArgs &, int, const float *, float);
 }  // namespace sf_gemv
 
 using namespace sf_gemv;
@@ -39,7 +42,8 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
   const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
   GemvArgs args{w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, L.G, has_zeros != 0,
                 (hipStream_t)stream};
-  // batch 4..8 with fp16 activations: the MFMA kernel (SF_GEMV_MFMA=0 keeps the VALU one)
+  // batch 3..8, fp16 activations, groups of 64 or 128: the MFMA kernel
+  // (SF_GEMV_MFMA=0 keeps the VALU one)
   static const bool mfma_ok = [] {
     const char *e = getenv("SF_GEMV_MFMA");
     return !(e && e[0] == '0');
@@ -65,4 +69,42 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
     }
   }
   return sf_check_launch("sf_q4_gemv");
+}
+
+extern "C" int sf_q4_gemv_fused(const void *blob, const float *src, int op, const float *norm_w,
+                                float eps, int act_dtype, void *y, int y_dtype, float *y_f32,
+                                const void *bias, int bias_dtype, int N, int K, int group_size,
+                                int has_zeros, void *stream) {
+  SF_REQUIRE(N > 0 && K > 0 && group_size > 0, SF_EINVAL, "invalid shape N=%d K=%d group_size=%d",
+             N, K, group_size);
+  SF_REQUIRE(K % group_size == 0, SF_EINVAL, "in_features must be divisible by group_size");
+  SF_REQUIRE(group_size % 32 == 0, SF_EUNSUPPORTED,
+             "group_size=%d: this build's kernels need a multiple of 32", group_size);
+  SF_REQUIRE(op == SF_PRE_RMSNORM || op == SF_PRE_SILU_MUL, SF_EINVAL, "bad fused op %d", op);
+  SF_REQUIRE(blob && src && (y || y_f32) && (op != SF_PRE_RMSNORM || norm_w), SF_EINVAL,
+             "null pointer argument");
+  SF_REQUIRE(act_dtype == SF_F16 || act_dtype == SF_BF16 || act_dtype == SF_F32, SF_EINVAL,
+             "bad activation dtype %d", act_dtype);
+  SF_REQUIRE(y_dtype == SF_F16 || y_dtype == SF_BF16 || y_dtype == SF_F32, SF_EINVAL,
+             "bad output dtype %d", y_dtype);
+  SF_REQUIRE(!bias || bias_dtype == SF_F16 || bias_dtype == SF_BF16 || bias_dtype == SF_F32,
+             SF_EINVAL, "bad bias dtype %d", bias_dtype);
+  SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)src & 15) == 0 &&
+                 ((uintptr_t)norm_w & 15) == 0,
+             SF_EINVAL, "blob must be 256-byte aligned, src and norm_w 16-byte aligned");
+  BlobLayout L;
+  sf_blob_layout(N, K, group_size, has_zeros, &L);
+  GemvPlan pl;
+  int rc = plan_gemv(1, N, K, group_size, act_dtype, &pl, 8);
+  if (rc) return rc;
+  const uint8_t *w = (const uint8_t *)blob;
+  const f16 *st = (const f16 *)(w + L.s_off);
+  const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
+  GemvArgs args{w, st, zt, src, y, y_dtype, y_f32, bias, bias_dtype, 1, N, K, L.G, has_zeros != 0,
+                (hipStream_t)stream};
+  const int pre = op == SF_PRE_RMSNORM ? PRE_RMSNORM : PRE_SILU;
+  if (act_dtype == SF_F16) launch_pre<SF_F16>(pl, args, pre, norm_w, eps);
+  else if (act_dtype == SF_BF16) launch_pre<SF_BF16>(pl, args, pre, norm_w, eps);
+  else launch_pre<SF_F32>(pl, args, pre, norm_w, eps);
+  return sf_check_launch("sf_q4_gemv_fused");
 }

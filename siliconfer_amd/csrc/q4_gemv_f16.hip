@@ -4,4 +4,5 @@
 
 namespace sf_gemv {
 template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
+template void launch_pre<SF_F16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
 }  // namespace sf_gemv

@@ -167,8 +167,7 @@ struct Act;
 template <>
 struct Act<SF_F16> {
   half2_t p[16];
-  __device__ __forceinline__ void load(const void *x, size_t off) {
-    const u32x4 *xq = (const u32x4 *)((const f16 *)x + off);
+  __device__ __forceinline__ void build(const u32x4 (&xq)[4]) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const u32x4 v = xq[q4];
@@ -180,6 +179,19 @@ struct Act<SF_F16> {
       p[4 * q4 + 3] = half2_t{b.y, d.y};
     }
   }
+  __device__ __forceinline__ void load(const void *x, size_t off) {
+    const u32x4 *xq = (const u32x4 *)((const f16 *)x + off);
+    const u32x4 v[4] = {xq[0], xq[1], xq[2], xq[3]};
+    build(v);
+  }
+  // from fp32 values, rounded as an fp16 activation buffer would hold them
+  __device__ __forceinline__ void from_f32(const float (&f)[32]) {
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[i / 4][i % 4] = sf_bitcast<uint32_t>(half2_t{(f16)f[2 * i], (f16)f[2 * i + 1]});
+    build(v);
+  }
 };
 
 __device__ __forceinline__ uint32_t pair_lo_lo(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
@@ -189,8 +201,7 @@ template <>
 struct Act<SF_BF16> {
   bf16x2_t p[16];
   float sum;  // sum of the 32 activations (exact bf16 values, fp32 adds)
-  __device__ __forceinline__ void load(const void *x, size_t off) {
-    const u32x4 *xq = (const u32x4 *)((const uint16_t *)x + off);
+  __device__ __forceinline__ void build(const u32x4 (&xq)[4]) {
     sum = 0.f;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
@@ -204,25 +215,35 @@ struct Act<SF_BF16> {
         sum += sf_bitcast<float>(v[i] << 16) + sf_bitcast<float>(v[i] & 0xFFFF0000u);
     }
   }
+  __device__ __forceinline__ void load(const void *x, size_t off) {
+    const u32x4 *xq = (const u32x4 *)((const uint16_t *)x + off);
+    const u32x4 v[4] = {xq[0], xq[1], xq[2], xq[3]};
+    build(v);
+  }
+  __device__ __forceinline__ void from_f32(const float (&f)[32]) {
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[i / 4][i % 4] = (uint32_t)sf_f32_to_bf16(f[2 * i]) | ((uint32_t)sf_f32_to_bf16(f[2 * i + 1]) << 16);
+    build(v);
+  }
 };
 
 template <>
 struct Act<SF_F32> {
   bf16x2_t hi[16], lo[16];
   float sum;  // sum of (hi + lo) over the 32 activations
-  __device__ __forceinline__ void load(const void *x, size_t off) {
-    const float4_t *xq = (const float4_t *)((const float *)x + off);
+  __device__ __forceinline__ void from_f32(const float (&f)[32]) {
     sum = 0.f;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const float4_t a = xq[2 * q4], b = xq[2 * q4 + 1];  // x[8q4 .. 8q4+8)
-      float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       uint16_t h[8], l[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        h[i] = sf_f32_to_bf16(v[i]);
+        const float v = f[8 * q4 + i];
+        h[i] = sf_f32_to_bf16(v);
         const float hf = sf_bf16_to_f32(h[i]);
-        l[i] = sf_f32_to_bf16(v[i] - hf);
+        l[i] = sf_f32_to_bf16(v - hf);
         sum += hf + sf_bf16_to_f32(l[i]);
       }
 #pragma unroll
@@ -231,6 +252,16 @@ struct Act<SF_F32> {
         lo[4 * q4 + j] = sf_bitcast<bf16x2_t>((uint32_t)l[j] | ((uint32_t)l[j + 4] << 16));
       }
     }
+  }
+  __device__ __forceinline__ void load(const void *x, size_t off) {
+    const float4_t *xq = (const float4_t *)((const float *)x + off);
+    float f[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4_t v = xq[i];
+      f[4 * i] = v.x; f[4 * i + 1] = v.y; f[4 * i + 2] = v.z; f[4 * i + 3] = v.w;
+    }
+    from_f32(f);
   }
 };
 
@@ -276,12 +307,21 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &wq, uint32_t z, const Ac
   }
 }
 
-template <int B, int R, int Q, bool ASYM, int XDT>
+// PRE (batch 1 only) folds the producer of x into the activation load: x is
+// then the fp32 source row and each lane builds its 32 activations itself,
+// rounded to XDT exactly as sf_rmsnorm / sf_silu_mul would store them
+// (PRE_RMSNORM: src * inv_rms(src) * pre_w, the norm from sf_row_inv_rms;
+// PRE_SILU: silu(src[k]) * src[K + k]). Every lane then issues its loads at
+// clamped positions, so the norm's wave reduction runs with all lanes active.
+constexpr int PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SILU = 2;
+
+template <int B, int R, int Q, bool ASYM, int XDT, int PRE = PRE_NONE>
 __global__ void __launch_bounds__(512)
 k_q4_gemv(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
           const uint8_t *__restrict__ ztile, const void *__restrict__ x, void *__restrict__ y,
           int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt, int N, int K,
-          int G, int cpg_shift, int C, int P, int RS) {
+          int G, int cpg_shift, int C, int P, int RS, const float *__restrict__ pre_w, float eps) {
+  static_assert(PRE == PRE_NONE || B == 1, "folded producers are batch-1 only");
   __shared__ float red[8][B * R];
   const int tid = threadIdx.x;
   const int rs = tid / P;
@@ -295,7 +335,61 @@ k_q4_gemv(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
 
-  if (c < C && row0 < N) {
+  if constexpr (PRE != PRE_NONE) {
+    const bool valid = c < C && row0 < N;
+    const int cc = min(c, C - 1);
+    const int grp = cc >> cpg_shift;
+    const size_t cell = (size_t)(min(row0, N - 1) >> 3) * G + grp;
+    float sc[R];
+    load_scales<R>(stile + cell * 8, (size_t)G * 8, row0, N, sc);
+    uint64_t zn = 0x8888888888888888ull;
+    if constexpr (ASYM) zn = load_zeros<R>(ztile + cell * 4, (size_t)G * 4, row0, N);
+    const float *src = (const float *)x;
+    // the norm's row loads first: its sum then needs none of the weights
+    // (the host checks K % 32 == 0 and a 16-byte aligned row)
+    SfRowNorm norm;
+    if constexpr (PRE == PRE_RMSNORM) norm.issue<true>(src, nullptr, K);
+    float f[32], g2[32];
+    {
+      // PRE_SILU: gate and up; PRE_RMSNORM: the row chunk and its norm weights
+      const float4_t *a = (const float4_t *)(src + (size_t)cc * 32);
+      const float4_t *b = PRE == PRE_SILU ? (const float4_t *)(src + K + (size_t)cc * 32)
+                                          : (const float4_t *)(pre_w + (size_t)cc * 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float4_t u = a[i], v = b[i];
+        f[4 * i] = u.x; f[4 * i + 1] = u.y; f[4 * i + 2] = u.z; f[4 * i + 3] = u.w;
+        g2[4 * i] = v.x; g2[4 * i + 1] = v.y; g2[4 * i + 2] = v.z; g2[4 * i + 3] = v.w;
+      }
+    }
+    u32x4 wv[R];
+    const uint8_t *wp = w + (size_t)cc * 16;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, N - 1);
+      wv[r] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)row * Kh));
+    }
+    // the weight stream goes out before the activation math (the scheduler
+    // would otherwise move the loads below it to save registers)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRE == PRE_RMSNORM) {
+      const float inv = norm.finish(src, nullptr, K, eps);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) f[i] = sf_opaque(f[i] * inv * g2[i]);  // as k_rmsnorm
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) f[i] = sf_silu_mul(f[i], g2[i]);
+    }
+    Act<XDT> xa;
+    xa.from_f32(f);
+    // no branch on `valid` (the compiler would sink the weight loads into it)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t z = (uint32_t)(zn >> (4 * r)) & 15u;
+      const float d = chunk_dot<XDT>(wv[r], z, xa) * sc[r];
+      acc[0][r] = valid ? d : 0.f;
+    }
+  } else if (c < C && row0 < N) {
     // small, cache-resident operands first, then the weight stream, so each
     // row's math can start as soon as its own 16 bytes arrive
     const int grp = c >> cpg_shift;
@@ -391,26 +485,29 @@ inline int pick_rows(int B, int xdt) {
   return r;
 }
 
-inline int plan_gemv(int B, int N, int K, int g, int xdt, GemvPlan *pl) {
+inline int plan_gemv(int B, int N, int K, int g, int xdt, GemvPlan *pl, int rows = 0) {
   pl->C = K / 32;
   pl->P = pl->C <= 32 ? 32 : ((pl->C + 63) / 64) * 64;
   SF_REQUIRE(pl->P <= 512, SF_EUNSUPPORTED, "in_features=%d exceeds this GEMV's limit of 16384", K);
   pl->Q = pl->P == 32 ? 32 : 64;
-  pl->WG = pl->P <= 256 ? 256 : pl->P;
+  // rowsets of P lanes fill a 256-thread group when P divides 256; otherwise
+  // one rowset per group (no idle waves)
+  pl->WG = 256 % pl->P == 0 ? 256 : pl->P;
   pl->RS = pl->WG / pl->P;
-  pl->R = pick_rows(B, xdt);
+  pl->R = rows ? rows : pick_rows(B, xdt);
   const int rows_per_wg = pl->RS * pl->R;
   pl->grid = (N + rows_per_wg - 1) / rows_per_wg;
   pl->cpg_shift = ilog2(g / 32);
   return SF_OK;
 }
 
-template <int B, int R, int Q, bool A, int X>
+template <int B, int R, int Q, bool A, int X, int PRE = PRE_NONE>
 void launch_t(const GemvPlan &pl, const uint8_t *w, const f16 *st, const uint8_t *zt, const void *x,
               void *y, int ydt, float *y32, const void *bias, int bdt, int N, int K, int G,
-              hipStream_t s) {
-  k_q4_gemv<B, R, Q, A, X><<<pl.grid, pl.WG, 0, s>>>(w, st, zt, x, y, ydt, y32, bias, bdt, N, K,
-                                                     G, pl.cpg_shift, pl.C, pl.P, pl.RS);
+              hipStream_t s, const float *pre_w = nullptr, float eps = 0.f) {
+  k_q4_gemv<B, R, Q, A, X, PRE><<<pl.grid, pl.WG, 0, s>>>(w, st, zt, x, y, ydt, y32, bias, bdt, N,
+                                                          K, G, pl.cpg_shift, pl.C, pl.P, pl.RS,
+                                                          pre_w, eps);
 }
 
 template <int B, int R, int X>
@@ -463,6 +560,28 @@ void launch_x(const GemvPlan &pl, const GemvArgs &a) {
       default: launch_b<8, X>(pl, a); break;
     }
   }
+}
+
+// Batch-1 GEMV with a folded producer (PRE_RMSNORM / PRE_SILU); the plan has R = 8.
+template <int X>
+void launch_pre(const GemvPlan &pl, const GemvArgs &a, int pre, const float *pre_w, float eps) {
+#define SF_PRE_T(Q, A, P)                                                                       \
+  launch_t<1, 8, Q, A, X, P>(pl, a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.N, a.K, \
+                             a.G, a.s, pre_w, eps)
+#define SF_PRE_QA(P)                          \
+  do {                                        \
+    if (pl.Q == 64) {                         \
+      if (a.asym) SF_PRE_T(64, true, P);      \
+      else SF_PRE_T(64, false, P);            \
+    } else {                                  \
+      if (a.asym) SF_PRE_T(32, true, P);      \
+      else SF_PRE_T(32, false, P);            \
+    }                                         \
+  } while (0)
+  if (pre == PRE_RMSNORM) SF_PRE_QA(PRE_RMSNORM);
+  else SF_PRE_QA(PRE_SILU);
+#undef SF_PRE_QA
+#undef SF_PRE_T
 }
 
 }  // namespace sf_gemv

@@ -132,4 +132,126 @@ __device__ __forceinline__ void sf_store_from_f32(void *p, size_t i, float v) {
   else ((uint16_t *)p)[i] = sf_f32_to_bf16(v);
 }
 
+// v as an fp32 value in a register. A product converted to fp16 right away
+// can otherwise become one v_fma_mixlo_f16 (a single rounding instead of fp32
+// then fp16), whatever the contraction setting; every kernel that rounds a
+// product to an activation dtype goes through this, so the folded and unfolded
+// decoder paths agree bit for bit.
+__device__ __forceinline__ float sf_opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// v rounded to DT and back: the value a DT buffer would hand the next kernel.
+template <int DT>
+__device__ __forceinline__ float sf_round_as(float v) {
+  v = sf_opaque(v);
+  if constexpr (DT == SF_F32) return v;
+  else if constexpr (DT == SF_F16) return (float)(f16)v;
+  else return sf_bf16_to_f32(sf_f32_to_bf16(v));
+}
+
 __device__ __forceinline__ float sf_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+template <int CTRL>
+__device__ __forceinline__ float sf_dpp(float v) {
+  return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the same bits (each step
+// adds a value and its butterfly partner, and fp addition commutes).
+__device__ __forceinline__ float sf_wave_sum(float v) {
+  v += sf_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += sf_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += sf_dpp<0x141>(v);  // row_half_mirror
+  v += sf_dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// 1 / sqrt(mean((x + delta)^2) + eps) over one row of H fp32 values, computed
+// by one whole wave in a fixed order. Every kernel that normalises a row uses
+// this, so the RMSNorm kernel and the projections that fold the norm into
+// their activation load produce the same bits. All 64 lanes must be active.
+// With H % 4 == 0 and 16-byte aligned rows (VEC), lane l takes the float4s
+// l + 64 u (u = 0..7) of each pass of 512, all of a pass's loads before its
+// fmas (clamped indices, out-of-range values zeroed by a select); otherwise a
+// scalar loop. Then sf_wave_sum. issue() loads u = 0..3 of the first pass
+// early (a caller can put them ahead of its other loads); finish() continues
+// the same fma chain.
+struct SfRowNorm {
+  float4_t v[4];
+  bool vec;
+
+  template <bool ASSUME_VEC = false>
+  __device__ __forceinline__ void issue(const float *__restrict__ x, const float *__restrict__ delta,
+                                        int H) {
+    vec = ASSUME_VEC || ((H & 3) == 0 && ((uintptr_t)x & 15) == 0 &&
+                         (!delta || ((uintptr_t)delta & 15) == 0));
+    if (!vec) return;
+    const int lane = threadIdx.x & 63, n4 = H >> 2;
+    const float4_t *x4 = (const float4_t *)x, *d4 = (const float4_t *)delta;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(lane + 64 * u, n4 - 1);
+      v[u] = x4[i];
+      if (delta) v[u] += d4[i];
+    }
+  }
+
+  __device__ __forceinline__ float finish(const float *__restrict__ x,
+                                          const float *__restrict__ delta, int H, float eps) {
+    const int lane = threadIdx.x & 63;
+    float ss = 0.f;
+    if (vec) {
+      const int n4 = H >> 2;
+      const float4_t *x4 = (const float4_t *)x, *d4 = (const float4_t *)delta;
+      auto acc = [&](const float4_t &t0, bool in) {
+        const float4_t t = in ? t0 : float4_t{0.f, 0.f, 0.f, 0.f};
+        ss = fmaf(t.x, t.x, ss);
+        ss = fmaf(t.y, t.y, ss);
+        ss = fmaf(t.z, t.z, ss);
+        ss = fmaf(t.w, t.w, ss);
+      };
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc(v[u], lane + 64 * u < n4);
+      for (int base = 0; base < n4; base += 512) {
+        const int u0 = base == 0 ? 4 : 0;  // the first pass's u < 4 came from issue()
+        if (base + 64 * u0 >= n4) break;   // nothing left in range (adds only zeros)
+        float4_t w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = min(base + lane + 64 * u, n4 - 1);
+          w[u] = x4[i];
+          if (delta) w[u] += d4[i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u >= u0) acc(w[u], base + lane + 64 * u < n4);
+      }
+    } else {
+      for (int h = lane; h < H; h += 64) {
+        float t = x[h];
+        if (delta) t += delta[h];
+        ss = fmaf(t, t, ss);
+      }
+    }
+    ss = sf_wave_sum(ss);
+    return 1.f / sqrtf(ss / (float)H + eps);
+  }
+};
+
+__device__ __forceinline__ float sf_row_inv_rms(const float *__restrict__ x,
+                                                const float *__restrict__ delta, int H, float eps) {
+  SfRowNorm n;
+  n.issue(x, delta, H);
+  return n.finish(x, delta, H, eps);
+}
+
+// silu(g) * u as the decoder computes it (one formula for every kernel):
+// g * (1 / (1 + exp(-g))) * u with the hardware reciprocal (1 ulp) instead of
+// an IEEE division, which takes about ten instructions.
+__device__ __forceinline__ float sf_silu_mul(float g, float u) {
+  return sf_opaque(g * __builtin_amdgcn_rcpf(1.f + expf(-g)) * u);
+}

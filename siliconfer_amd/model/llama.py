@@ -92,7 +92,8 @@ class LlamaModel:
 
     def __init__(self, config: ModelConfig, layers: list[LayerWeights], embed: torch.Tensor,
                  norm_w: torch.Tensor, group_size: int, max_seq: int,
-                 act_dtype: torch.dtype = torch.float32, max_prefill: int = 512):
+                 act_dtype: torch.dtype = torch.float32, max_prefill: int = 512,
+                 fuse: bool = True):
         if embed.dtype != torch.bfloat16:
             raise SFError("the tied embedding must be bf16")
         if act_dtype not in _DT:
@@ -100,6 +101,9 @@ class LlamaModel:
         self.config, self.layers, self.embed, self.norm_w = config, layers, embed, norm_w
         self.group_size, self.max_seq, self.act_dtype = group_size, max_seq, act_dtype
         self.max_prefill = max_prefill
+        # decode folds each RMSNorm and the SwiGLU into the next projection
+        # (bit-identical to running them as separate kernels; fuse=False does)
+        self.fuse = fuse
         self.device = embed.device
         self.lib = _lib.load()
         c = config
@@ -144,7 +148,7 @@ class LlamaModel:
     @classmethod
     def random_init(cls, config: ModelConfig, seed: int = 4, group_size: int = 64,
                     device=None, max_seq: int = 1024, act_dtype: torch.dtype = torch.float32,
-                    std: float = 0.02, max_prefill: int = 512) -> "LlamaModel":
+                    std: float = 0.02, max_prefill: int = 512, fuse: bool = True) -> "LlamaModel":
         """Random weights N(0, std) drawn on the device from `seed` (RMSNorm
         weights 1, q/k/v biases N(0, std) when the config has attention bias),
         every projection RTN int4 symmetric with `group_size`, the tied
@@ -177,7 +181,7 @@ class LlamaModel:
             ones = torch.ones(H, dtype=torch.float32, device=dev)
             layers.append(LayerWeights(qkv, bias, o, gate_up, down, ones, ones.clone()))
         norm_w = torch.ones(H, dtype=torch.float32, device=dev)
-        return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill)
+        return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill, fuse)
 
     def export_weights(self) -> dict:
         """Host copies for a reference restatement: dequantized fp32 weights
@@ -228,6 +232,14 @@ class LlamaModel:
                                       int(w.has_zeros), None if ws is None else ws.data_ptr(),
                                       0 if ws is None else ws.numel(), self._st()), "sf_q4_gemm")
 
+    def _gemv_fused(self, w: Q4Weight, src: torch.Tensor, op: int, norm_w, y32: torch.Tensor,
+                    bias: torch.Tensor | None):
+        self._chk(self.lib.sf_q4_gemv_fused(
+            w.blob.data_ptr(), src.data_ptr(), op, None if norm_w is None else norm_w.data_ptr(),
+            float(self.config.rms_norm_eps), _DT[self.act_dtype], None, _lib.SF_F32, y32.data_ptr(),
+            None if bias is None else bias.data_ptr(), _lib.SF_F32, w.out_features, w.in_features,
+            w.group_size, int(w.has_zeros), self._st()), "sf_q4_gemv_fused")
+
     def _rmsnorm(self, x, delta, w, out, rows):
         self._chk(self.lib.sf_rmsnorm(x.data_ptr(), None if delta is None else delta.data_ptr(),
                                       w.data_ptr(), _lib.SF_F32, out.data_ptr(), _DT[out.dtype], rows,
@@ -239,6 +251,14 @@ class LlamaModel:
             _DT[q_out.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
             self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, rows, self.Hq,
             self.KVH, self.D, self.max_seq, pos_dev, pos_host, self._st()), "sf_rope_kv_append")
+
+    def _lm_head_norm(self, h_row, token, pos_inc, logits=True):
+        self._chk(self.lib.sf_lm_head_argmax_rmsnorm(
+            self.embed.data_ptr(), h_row.data_ptr(), self.norm_w.data_ptr(),
+            float(self.config.rms_norm_eps), _DT[self.act_dtype],
+            self.logits.data_ptr() if logits else None, self.V, self.H, token.data_ptr(), pos_inc,
+            self.hist.data_ptr() if pos_inc else None, self.head_ws.data_ptr(), self.head_ws.numel(),
+            self._st()), "sf_lm_head_argmax_rmsnorm")
 
     def _lm_head(self, x_row, token, pos_inc, logits=True):
         self._chk(self.lib.sf_lm_head_argmax(
@@ -324,9 +344,13 @@ class LlamaModel:
         pos = self.pos_dev.data_ptr()
         self._chk(lib.sf_embed(self.token.data_ptr(), self.embed.data_ptr(), _lib.SF_BF16,
                                self.h.data_ptr(), 1, self.H, self.V, st), "sf_embed")
+        fuse = self.fuse
         for l, L in enumerate(self.layers):
-            self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
-            self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
+            if fuse:  # RMSNorm folded into the projection's activation load
+                self._gemv_fused(L.qkv, self.h, _lib.SF_PRE_RMSNORM, L.w_in, self.qkv, L.qkv_bias)
+            else:
+                self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
+                self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
             self._rope_append(l, self.qkv, self.q, 1, pos, 0)
             self._chk(lib.sf_attn_decode_i8kv_dev(
                 self.q.data_ptr(), _DT[self.q.dtype], self.k_codes[l].data_ptr(),
@@ -335,13 +359,20 @@ class LlamaModel:
                 self.attn_ws.numel(), 1, self.Hq, self.KVH, pos, 1, self.max_seq, self.max_seq,
                 self.D, self.scale, self.attn_splits, st), "sf_attn_decode_i8kv_dev")
             self._gemv(L.o, self.attn, self.h, self.h)        # residual add as the bias
-            self._rmsnorm(self.h, None, L.w_post, self.xn, 1)
-            self._gemv(L.gate_up, self.xn, self.gu, None)
-            self._chk(lib.sf_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), _DT[self.act.dtype], 1,
-                                      self.I, st), "sf_silu_mul")
-            self._gemv(L.down, self.act, self.h, self.h)
-        self._rmsnorm(self.h, None, self.norm_w, self.xn, 1)
-        self._lm_head(self.xn, self.token, pos, logits=logits)
+            if fuse:  # RMSNorm, then SwiGLU, folded into the next projections
+                self._gemv_fused(L.gate_up, self.h, _lib.SF_PRE_RMSNORM, L.w_post, self.gu, None)
+                self._gemv_fused(L.down, self.gu, _lib.SF_PRE_SILU_MUL, None, self.h, self.h)
+            else:
+                self._rmsnorm(self.h, None, L.w_post, self.xn, 1)
+                self._gemv(L.gate_up, self.xn, self.gu, None)
+                self._chk(lib.sf_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), _DT[self.act.dtype],
+                                          1, self.I, st), "sf_silu_mul")
+                self._gemv(L.down, self.act, self.h, self.h)
+        if fuse:
+            self._lm_head_norm(self.h, self.token, pos, logits=logits)
+        else:
+            self._rmsnorm(self.h, None, self.norm_w, self.xn, 1)
+            self._lm_head(self.xn, self.token, pos, logits=logits)
 
     def capture(self, logits: bool = False) -> None:
         """Record one decode step as a HIP graph (positions and tokens are

@@ -116,3 +116,16 @@ def test_python_layer_raises_without_device():
     pk, s = K.pack_weights_sym(W, 64)
     with pytest.raises(RuntimeError):
         K.gemv_sym(pk, s, np.ones(64, np.float32), 64)
+
+
+def test_fused_gemv_rejects_bad_op_and_missing_norm_weight():
+    lib = _lib.load()
+    blob, src, y = 256 * 1024, 4096, 8192  # fake addresses: validation fails before any use
+    args = lambda op, nw, K=256: (blob, src, op, nw, 1e-6, _lib.SF_F16, None, _lib.SF_F32, y, None,
+                                  _lib.SF_F32, 64, K, 64, 0, None)
+    assert lib.sf_q4_gemv_fused(*args(7, 4096)) == -1
+    assert "fused op" in _lib.last_error()
+    assert lib.sf_q4_gemv_fused(*args(_lib.SF_PRE_RMSNORM, None)) == -1
+    assert "null pointer" in _lib.last_error()
+    assert lib.sf_q4_gemv_fused(*args(_lib.SF_PRE_SILU_MUL, None, K=100)) == -1
+    assert "divisible by group_size" in _lib.last_error()

@@ -1,7 +1,8 @@
 """GPU parity of the split-T decode attention over the int8 KV cache against the
 oracle (float64 dequantize-then-softmax), through the C ABI
 (sf_attn_decode_i8kv). Bar: 2e-3 relative.
-Reference tests restated: tests/test_metal_attention.py:45-183.
+Reference tests restated: tests/test_metal_attention.py:45-183. Each test runs
+on both kernels (the `kernel_choice` fixture).
 """
 
 import numpy as np
@@ -15,6 +16,15 @@ from siliconfer_amd.kernels.attention import (_choose_n_tiles, attention_decode,
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+
+
+@pytest.fixture(params=["mfma", "valu"], autouse=True)
+def kernel_choice(request, monkeypatch):
+    """Every test runs on both decode kernels: the MFMA one (up to 16 query
+    heads per kv head, head_dim 64 / 128) and the VALU one (SF_ATTN_MFMA=0,
+    read by the library on every call)."""
+    monkeypatch.setenv("SF_ATTN_MFMA", "1" if request.param == "mfma" else "0")
+    return request.param
 
 
 def make_inputs(rng, B, H, KVH, D, T, scale_dtype=np.float32):
@@ -185,3 +195,11 @@ def test_gqa_group_widths(dev, G):
     and groups split over several blocks)."""
     rng = np.random.default_rng(30 + G)
     check(dev, *make_inputs(rng, 2, 2 * G, 2, 64, 333), what=f"G={G}")
+
+
+@pytest.mark.parametrize("T,S", [(1, 1), (31, 1), (33, 2), (1000, 3), (777, 100)])
+def test_sixteen_heads_d128(dev, T, S):
+    """A full 16-head group at head_dim 128: partial 32-token tiles, splits
+    shorter than a tile, and many splits."""
+    rng = np.random.default_rng(40 + T)
+    check(dev, *make_inputs(rng, 1, 32, 2, 128, T), n_tiles=S, what=f"G=16 D=128 T={T} S={S}")

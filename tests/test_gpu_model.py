@@ -148,3 +148,30 @@ def test_qwen05b_geometry_matches_oracle(dev):
     m = LlamaModel.random_init(cfg, seed=4, group_size=64, device=dev, max_seq=64)
     ids = np.random.default_rng(4).integers(0, cfg.vocab_size, 32)
     check_against_oracle(m, cfg, ids, 3, 1e-2, "qwen0.5b")
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.float16])
+def test_folded_decode_equals_unfolded(dev, act):
+    """Decode with RMSNorm / SwiGLU folded into the projections gives the same
+    bits as the separate kernels (non-unit norm weights, several steps)."""
+    models = []
+    for fuse in (True, False):
+        m = LlamaModel.random_init(SMALL, seed=21, device=dev, max_seq=64, act_dtype=act, fuse=fuse)
+        g = torch.Generator(device=dev)
+        g.manual_seed(22)
+        for L in m.layers:
+            L.w_in.copy_(1 + 0.2 * torch.randn(L.w_in.shape, generator=g, device=dev))
+            L.w_post.copy_(1 + 0.2 * torch.randn(L.w_post.shape, generator=g, device=dev))
+        m.norm_w.copy_(1 + 0.2 * torch.randn(m.norm_w.shape, generator=g, device=dev))
+        models.append(m)
+    ids = np.random.default_rng(23).integers(0, SMALL.vocab_size, 11)
+    for m in models:
+        m.prefill(ids)
+    for _ in range(5):
+        outs = []
+        for m in models:
+            m.decode_step(logits=True)
+            m.pos += 1
+            torch.cuda.synchronize()
+            outs.append((m.logits.cpu().clone(), int(m.token.item())))
+        assert torch.equal(outs[0][0], outs[1][0]) and outs[0][1] == outs[1][1]
