@@ -583,42 +583,51 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint32_t lo, uint32_t hi) {
   return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-template <int D>
+template <int D, int NW>
 constexpr int attn_mfma_smem_floats() {
-  // main phase: V tiles [4][32][D + 8] bytes, then wave states m, l [4][16]
-  // and O [4][16][D]; merge phase: attn_merge_splits<16, kMfmaMaxSplits>
-  constexpr int a = kAttnWaves * 32 * (D + 8) / 4 + 2 * kAttnWaves * 16 + kAttnWaves * 16 * D;
-  constexpr int b = 4 * kAttnThreads + 2 * 16 * kMfmaMaxSplits + 16;
+  // main phase: V tiles [NW][32][D + 8] bytes, then wave states m, l [NW][16]
+  // and O [NW][16][D]; merge phase (4 waves only): attn_merge_splits<16, kMfmaMaxSplits>
+  constexpr int a = NW * 32 * (D + 8) / 4 + 2 * NW * 16 + NW * 16 * D;
+  constexpr int b = NW == kAttnWaves ? 4 * kAttnThreads + 2 * 16 * kMfmaMaxSplits + 16 : 0;
   return a > b ? a : b;
 }
 
-template <int QDT, int SDT, int D>
-__global__ void __launch_bounds__(kAttnThreads)
+// NW waves per workgroup, NB of a wave's tiles in flight. NW = 4 serves
+// split-T launches (the cross-split merge runs on 256 threads); NW = 8 serves
+// one split per (b, kv head): with 4 tiles per wave in flight (2 at head_dim
+// 128, for registers), a 1024-token cache is one round of loads and needs no
+// cross-workgroup merge.
+// Splits start on 32-token boundaries (tile rounded up to a multiple of 32), so
+// when T_cap % 4 == 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
+template <int QDT, int SDT, int D, int NW, int NB>
+__global__ void __launch_bounds__(NW * 64)
 k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
             const int8_t *__restrict__ vc, const void *__restrict__ vs, float *part_acc,
             float *part_ml, unsigned *counters, void *__restrict__ out, int odt, int H, int KVH,
             int T, const int *__restrict__ T_dev, int causal, int T_cap, float qscale,
-            int n_splits) {
+            int n_splits, int vscale) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  constexpr int NW = kAttnWaves;
+  static_assert(NW == kAttnWaves || NW == 8, "4 waves (split-T) or 8 (one split)");
+  constexpr int NT = NW * 64;
   constexpr int KS = D / 32;       // q.k k-steps per token
   constexpr int DB = D / 16;       // P V dim blocks
   constexpr int KW = D / 16;       // K dwords per lane per token (D/4 bytes)
   constexpr int VC = D / 32;       // 16-byte V chunks per lane per tile
   constexpr int PITCH = D + 8;     // V tile row pitch in LDS, bytes
   constexpr bool QSPLIT = QDT != SF_F16;
-  __shared__ __attribute__((aligned(16))) float smem[attn_mfma_smem_floats<D>()];
+  __shared__ __attribute__((aligned(16))) float smem[attn_mfma_smem_floats<D, NW>()];
   __shared__ int s_last;
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = H / KVH;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane & 15, g = lane >> 4;
   int Tv = T_dev ? *T_dev + T : T;
   if (causal) Tv = T + b + 1;
   Tv = max(0, min(Tv, T_cap));
-  const int tile = (Tv + n_splits - 1) / n_splits;
-  const int t0 = split * tile, t1 = min(t0 + tile, Tv);
+  const int tile = ((Tv + n_splits - 1) / n_splits + 31) & ~31;
+  const int t0 = min(split * tile, Tv), t1 = min(t0 + tile, Tv);
   const size_t base = ((size_t)(causal ? 0 : b) * KVH + kvh) * (size_t)T_cap;
   const size_t bh0 = (size_t)b * H + (size_t)kvh * G;
 
@@ -640,7 +649,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   struct Tile {
     u32x4 k[2][KW / 4];  // K dwords of tokens hl and 16 + hl
     u32x4 v[VC];         // V chunks for the LDS stage
-    float ks[8], vs[8];  // scales of the lane's tokens T_g
+    float ks[8], vs[8];  // scales of the lane's tokens T_g (as loaded; masked later)
   };
   const int ntiles = t1 > t0 ? (t1 - t0 + 31) / 32 : 0;
   auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
@@ -659,11 +668,40 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       const int t = min(tb + tok, t1 - 1);
       tl.v[c] = *(const u32x4 *)(vc + (base + t) * D + piece * 16);
     }
+    if (vscale) {
+      // tokens tb + 4g .. + 3 and tb + 16 + 4g .. + 3: aligned 4-token groups;
+      // a group past T_cap is moved back inside (its tokens are masked anyway)
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const size_t row = base + min(tb + tok_of(r), t1 - 1);
-      tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
-      tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const size_t row = base + min(tb + 16 * h2 + 4 * g, T_cap - 4);
+        if constexpr (SDT == SF_F16) {
+          const u32x2 a = *(const u32x2 *)((const f16 *)ks + row);
+          const u32x2 c = *(const u32x2 *)((const f16 *)vs + row);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const half2_t ka = sf_bitcast<half2_t>(a[i]), va = sf_bitcast<half2_t>(c[i]);
+            tl.ks[4 * h2 + 2 * i] = (float)ka.x;
+            tl.ks[4 * h2 + 2 * i + 1] = (float)ka.y;
+            tl.vs[4 * h2 + 2 * i] = (float)va.x;
+            tl.vs[4 * h2 + 2 * i + 1] = (float)va.y;
+          }
+        } else {
+          const float4_t a = *(const float4_t *)((const float *)ks + row);
+          const float4_t c = *(const float4_t *)((const float *)vs + row);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            tl.ks[4 * h2 + i] = a[i];
+            tl.vs[4 * h2 + i] = c[i];
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const size_t row = base + min(tb + tok_of(r), t1 - 1);
+        tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
+        tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
+      }
     }
   };
 
@@ -708,7 +746,8 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     for (int r = 0; r < 8; ++r) {
       const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
       ps += p;
-      const float pv = p * tl.vs[r];
+      // masked tokens weigh exactly 0 (their scale may be any stale value)
+      const float pv = tb + tok_of(r) < t1 ? p * tl.vs[r] : 0.f;
       ph[r] = (f16)pv;
       pl[r] = (f16)(pv - (float)ph[r]);
     }
@@ -734,15 +773,21 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     }
   };
 
-  if (wave < ntiles) {
-    Tile b0, b1;
-    load(wave, b0);
-    for (int j = wave; j < ntiles; j += 2 * NW) {
-      if (j + NW < ntiles) load(j + NW, b1);
-      compute(j, b0);
-      if (j + NW >= ntiles) break;
-      if (j + 2 * NW < ntiles) load(j + 2 * NW, b0);
-      compute(j + NW, b1);
+  // this wave's tiles j = wave + NW i, i < mine; NB of them in flight (slot
+  // i % NB, compile-time after unrolling)
+  const int mine = wave < ntiles ? (ntiles - wave + NW - 1) / NW : 0;
+  Tile tl[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (u < mine) load(wave + NW * u, tl[u]);
+  for (int i0 = 0; i0 < mine; i0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int i = i0 + u;
+      if (i < mine) {
+        compute(wave + NW * i, tl[u]);
+        if (i + NB < mine) load(wave + NW * (i + NB), tl[u]);
+      }
     }
   }
   lsum += __shfl_xor(lsum, 16, 64);
@@ -763,7 +808,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   __syncthreads();
   const bool single = n_splits == 1;
   constexpr int NQ = D / 4;
-  for (int it = tid; it < G * NQ; it += kAttnThreads) {
+  for (int it = tid; it < G * NQ; it += NT) {
     const int h = it / NQ, d4 = (it - h * NQ) * 4;
     float M = -INFINITY;
 #pragma unroll
@@ -797,10 +842,12 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       }
     }
   }
-  if (single) return;
-  attn_merge_splits<16, kMfmaMaxSplits>(smem, &s_last, part_acc, part_ml,
-                                        counters + (size_t)b * KVH + kvh, bh0, G, D, n_splits,
-                                        out, odt);
+  if constexpr (NW == kAttnWaves) {
+    if (single) return;
+    attn_merge_splits<16, kMfmaMaxSplits>(smem, &s_last, part_acc, part_ml,
+                                          counters + (size_t)b * KVH + kvh, bh0, G, D, n_splits,
+                                          out, odt);
+  }
 }
 
 int pow2_log2_at_least(int v) {
@@ -877,13 +924,15 @@ extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
 }
 
 extern "C" int sf_attn_default_splits(int B, int KVH, int T) {
-  // About 128 tokens per split (one batch of 4 rows per wave at head_dim
-  // 64), at most 64 splits so that the final merge's loads of the partials
-  // all go out at once. Measured on MI355X at B = 1, 2 kv heads: 32 splits
-  // for T = 4096 and 64 for T = 16384 are the fastest of 1..128.
+  // Up to 1024 tokens: one split (one 8-wave workgroup per kv head holds the
+  // whole cache in one round of loads; no cross-workgroup merge). Beyond:
+  // about 128 tokens per split, at most 64 splits so that the final merge's
+  // loads of the partials all go out at once. Measured on MI355X at B = 1,
+  // 2 kv heads: 32 splits for T = 4096 and 64 for T = 16384 are the fastest
+  // of 1..128.
   (void)B;
   (void)KVH;
-  if (T <= 0) return 1;
+  if (T <= 1024) return 1;
   int s = (T + 127) / 128;
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
@@ -941,15 +990,23 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
                "attention batch too large for one call (B * n_kv_heads = %d > %d)", B * KVH,
                kMaxCounters);
     dim3 grid(n_splits, KVH, B);
-#define SF_MFMA_LAUNCH(QD, SD, DD)                                                              \
-  k_attn_mfma<QD, SD, DD><<<grid, kAttnThreads, 0, st>>>(q, k_codes, k_scales, v_codes, v_scales, \
-                                                         part_acc, part_ml, counters, out,       \
-                                                         out_dtype, H, KVH, T, T_dev, causal,    \
-                                                         T_cap, qscale, n_splits)
-#define SF_MFMA_D(QD, SD)                     \
-  do {                                        \
-    if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64);  \
-    else SF_MFMA_LAUNCH(QD, SD, 128);         \
+    // scale loads in aligned groups of 4 tokens when every row start allows it
+    const size_t sal = scale_dtype == SF_F16 ? 8 : 16;
+    const int vscale = T_cap % 4 == 0 && (uintptr_t)k_scales % sal == 0 &&
+                       (uintptr_t)v_scales % sal == 0;
+#define SF_MFMA_LAUNCH(QD, SD, DD, NWV, NBV)                                                     \
+  k_attn_mfma<QD, SD, DD, NWV, NBV><<<grid, NWV * 64, 0, st>>>(                                  \
+      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H,   \
+      KVH, T, T_dev, causal, T_cap, qscale, n_splits, vscale)
+#define SF_MFMA_D(QD, SD)                                   \
+  do {                                                      \
+    if (n_splits == 1) {                                    \
+      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, 8, 4);        \
+      else SF_MFMA_LAUNCH(QD, SD, 128, 8, 2);               \
+    } else {                                                \
+      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, kAttnWaves, 2); \
+      else SF_MFMA_LAUNCH(QD, SD, 128, kAttnWaves, 2);      \
+    }                                                       \
   } while (0)
     if (scale_dtype == SF_F16) {
       if (q_dtype == SF_F32) SF_MFMA_D(SF_F32, SF_F16);

@@ -94,6 +94,7 @@ def test_attention_validation_and_sizes():
     assert lib.sf_attn_default_splits(1, 2, 16384) == 64
     assert lib.sf_attn_default_splits(1, 2, 4096) == 32
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
+    assert lib.sf_attn_default_splits(1, 2, 1024) == 1 and lib.sf_attn_default_splits(1, 2, 1025) == 9
 
 
 def test_kv_append_validation():
