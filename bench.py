@@ -441,54 +441,111 @@ def profile_kernels(dev) -> None:
 def _short_kernel(name: str) -> str:
     import re
 
-    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)", name)
+    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)(?:ELi(\d))?", name)
     if m:
-        return f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},x={m.group(5)}>"
+        pre = {None: "", "0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(6)]
+        return (f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},"
+                f"x={m.group(5)}{pre}>")
+    m = re.search(r"k_q4_gemv_mfmaILi(\d+)ELb(\d)ELi(\d+)", name)
+    if m:
+        return f"k_q4_gemv_mfma<LW={m.group(1)},asym={m.group(2)},BPW={m.group(3)}>"
     m = re.search(r"(k_[a-z0-9_]+|__amd_rocclr_[A-Za-z]+|at::native::[a-z_]+)", name)
     return m.group(1) if m else name[:40]
 
 
+def sweep_launch_plan():
+    """(N, K, B, launches) of `--profile-kernels` in launch order: each sweep case
+    once per cold copy of its blob (the count GpuSweep's cold_copies makes)."""
+    plan = []
+    for N, K in SHAPES:
+        blob = -(-(N * K // 2) // 256) * 256 + -(-N // 8) * (K // GROUP) * 16
+        n = max(2, -(-COLD_BYTES // blob))
+        plan += [(N, K, B, n) for B in BATCHES]
+    return plan
+
+
 def summarize_profile(trace_csv=None, fetch_csv=None, write_csv=None) -> dict:
-    """Summaries of rocprofv3 CSV outputs of `bench.py --profile-kernels`:
-    per (kernel, grid) duration stats from a --kernel-trace run, and per
-    (kernel, grid) HBM bytes from FETCH_SIZE / WRITE_SIZE runs, scaled by what
-    the counters read for the 256 MiB calibration copy (the largest copy)."""
+    """Summaries of rocprofv3 CSV outputs of `bench.py --profile-kernels`: the
+    sweep's GEMV dispatches (the first ones of either GEMV kernel, in launch
+    order) labelled with their case by sweep_launch_plan(); per-case duration
+    stats from a --kernel-trace run, and per-case HBM bytes from FETCH_SIZE /
+    WRITE_SIZE runs, scaled by what the counters read for the 256 MiB
+    calibration copy (the largest copy dispatch)."""
     import csv
     import statistics
 
-    out = {}
+    plan = sweep_launch_plan()
+    labels = [(N, K, B) for N, K, B, n in plan for _ in range(n)]
+
+    def sweep_rows(rows, id_key):
+        gemv = sorted((r for r in rows if "k_q4_gemv" in r["Kernel_Name"]), key=lambda r: int(r[id_key]))
+        return list(zip(labels, gemv[:len(labels)]))
+
+    out = {"cases": [{"N": N, "K": K, "B": B, "launches": n} for N, K, B, n in plan]}
     if trace_csv:
-        agg = {}
-        for r in csv.DictReader(open(trace_csv)):
-            key = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]),
-                   int(r["Workgroup_Size_X"]))
-            agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-        out["durations_us"] = [
-            {"kernel": k[0], "grid_threads": k[1], "wg": k[2], "n": len(v),
-             "mean": round(statistics.fmean(v), 3), "median": round(statistics.median(v), 3),
-             "min": round(min(v), 3)} for k, v in agg.items() if len(v) >= 2]
+        rows = list(csv.DictReader(open(trace_csv)))
+        per = {}
+        for lab, r in sweep_rows(rows, "Dispatch_Id"):
+            per.setdefault(lab, (_short_kernel(r["Kernel_Name"]), []))[1].append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        for c in out["cases"]:
+            k, v = per.get((c["N"], c["K"], c["B"]), ("", []))
+            if v:
+                c.update(kernel=k, n=len(v), mean_us=round(statistics.fmean(v), 3),
+                         median_us=round(statistics.median(v), 3), min_us=round(min(v), 3))
+        copies = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
+                  if "copyBuffer" in r["Kernel_Name"]]
+        if copies:
+            out["copy_us"] = {"n": len(copies), "median": round(statistics.median(copies), 3),
+                              "max": round(max(copies), 3)}
     if fetch_csv and write_csv:
         def load(p):
-            agg = {}
-            for r in csv.DictReader(open(p)):
-                key = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size"]))
-                agg.setdefault(key, []).append(float(r["Counter_Value"]))
-            return agg
-        f, w = load(fetch_csv), load(write_csv)
-        # the calibration copy is the largest copy dispatch in the run
-        copy_kib = (256 << 20) / 1024
-        ff = copy_kib / max(v for k, vs in f.items() if "copyBuffer" in k[0] for v in vs)
-        wf = copy_kib / max(v for k, vs in w.items() if "copyBuffer" in k[0] for v in vs)
-        rows = []
-        for k in f:
-            if k not in w or "copyBuffer" in k[0]:
-                continue
-            rows.append({"kernel": k[0], "grid_threads": k[1], "n": len(f[k]),
-                         "fetch_bytes": int(statistics.median(f[k]) * ff * 1024),
-                         "write_bytes": int(statistics.median(w[k]) * wf * 1024)})
-        out["hbm_traffic"] = {"fetch_scale": round(ff, 4), "write_scale": round(wf, 4),
-                              "calibration": "256 MiB device copy", "per_launch": rows}
+            rows = list(csv.DictReader(open(p)))
+            val = {int(r["Dispatch_Id"]): float(r["Counter_Value"]) for r in rows}
+            copy_kib = max(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"])
+            per = {}
+            for lab, r in sweep_rows(rows, "Dispatch_Id"):
+                per.setdefault(lab, []).append(val[int(r["Dispatch_Id"])])
+            return per, copy_kib
+        (f, fk), (w, wk) = load(fetch_csv), load(write_csv)
+        ff, wf = (256 << 20) / 1024 / fk, (256 << 20) / 1024 / wk
+        for c in out["cases"]:
+            lab = (c["N"], c["K"], c["B"])
+            if lab in f and lab in w:
+                c["fetch_bytes"] = int(statistics.median(f[lab]) * ff * 1024)
+                c["write_bytes"] = int(statistics.median(w[lab]) * wf * 1024)
+                c["hbm_bytes"] = c["fetch_bytes"] + c["write_bytes"]
+                c["alg_bytes"] = alg_bytes(*lab)
+                c["hbm_over_alg"] = round(c["hbm_bytes"] / c["alg_bytes"], 4)
+        hb = [c["hbm_bytes"] for c in out["cases"] if "hbm_bytes" in c]
+        out["fetch_scale"], out["write_scale"] = round(ff, 4), round(wf, 4)
+        if hb:
+            out["hbm_bytes_per_launch_avg"] = int(statistics.fmean(hb))
     return out
+
+
+def summarize_e2e(trace_csv: str, steps: int = 8) -> dict:
+    """Per-kernel time per decoded token from a rocprofv3 --kernel-trace run of
+    `bench.py --profile-e2e`: the dispatches from the k_embed of the first of
+    the last `steps` decode steps on, grouped by kernel."""
+    import csv
+    import re
+    import statistics
+
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if "k_embed" in r["Kernel_Name"]]
+    dec = rows[starts[-steps]:]
+    per = {}
+    for r in dec:
+        name = r["Kernel_Name"]
+        m = re.search(r"(k_[a-z0-9_]+)(?:<([^>]*)>|I(\S+?)EEEv)?", name.replace("(anonymous namespace)::", ""))
+        key = _short_kernel(name) if "k_q4_gemv" in name else (m.group(1) + (f"<{m.group(2)}>" if m and m.group(2) else "") if m else name[:40])
+        per.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [{"kernel": k, "per_token": len(v) // steps, "mean_us": round(statistics.fmean(v), 3),
+            "min_us": round(min(v), 3), "us_per_token": round(sum(v) / steps, 1)}
+           for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1]))]
+    return {"steps": steps, "kernels": out,
+            "kernel_us_per_token": round(sum(sum(v) for v in per.values()) / steps, 1)}
 
 
 def load_traffic():
@@ -514,10 +571,15 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run eager launches of every case (for rocprofv3)")
+    ap.add_argument("--summarize-e2e", metavar="CSV",
+                    help="per-kernel time per token from a kernel trace of --profile-e2e")
     ap.add_argument("--summarize-profile", nargs="+", metavar="CSV",
                     help="TRACE_CSV [FETCH_CSV WRITE_CSV]: summarize rocprofv3 output and exit")
     args = ap.parse_args()
 
+    if args.summarize_e2e:
+        print(json.dumps(summarize_e2e(args.summarize_e2e), indent=1))
+        return 0
     if args.summarize_profile:
         paths = args.summarize_profile + [None] * 3
         print(json.dumps(summarize_profile(*paths[:3]), indent=1))
@@ -606,8 +668,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "k_q4_gemv via sf_q4_gemv; average over the 12 sweep cases, each timed "
-                      "as a graph of back-to-back cold launches between HIP events",
+            "kernel": "sf_q4_gemv (k_q4_gemv at batch 1-2, k_q4_gemv_mfma at batch 4-8); average "
+                      "over the 12 sweep cases, each timed as a graph of back-to-back cold launches "
+                      "between HIP events",
             "alg_bytes_per_launch_avg": int(sum(case_bytes) / len(case_bytes)),
         },
         "cases": cases,
