@@ -18,7 +18,7 @@ and an int8 KV cache:
   MLP               layers.py:136-144: down(silu(gate(x)) * up(x))
   block             layers.py:157-163: x + attn(norm(x)); x + mlp(norm(x))
   model             llama.py:55-79: embedding, blocks, final norm, logits
-                    through the tied embedding (as_linear)
+                    through the tied embedding (as_linear) or lm_head
   greedy            generate.py:45-46: argmax of the last row
 
 Weights come dequantized (fp32 codes * fp16 scale) from
@@ -127,7 +127,7 @@ def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: n
         act = (g / (np.float32(1.0) + np.exp(-g))) * u
         x = x + act @ L["down"].T
     xn = rmsnorm(x, weights["norm"], eps)
-    return (xn @ weights["embed"].T).astype(np.float32)
+    return (xn @ weights.get("lm_head", weights["embed"]).T).astype(np.float32)
 
 
 def greedy(logits_row: np.ndarray) -> int:

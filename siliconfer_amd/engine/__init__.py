@@ -1,0 +1,11 @@
+"""Model loading: HuggingFace safetensors checkpoints (the reference's
+siliconfer.engine.loader) and the int4 packing / packed on-disk format (its
+siliconfer.engine.q4_loader)."""
+
+from .loader import load_model, load_weights, weight_summary
+from .q4_loader import (PROJECTIONS, build_model, load_q4_model, load_q4_packed,
+                        pack_and_replace_linears, packing_symmetry, save_q4_model)
+
+__all__ = ["load_model", "load_weights", "weight_summary", "PROJECTIONS", "build_model",
+           "load_q4_model", "load_q4_packed", "pack_and_replace_linears", "packing_symmetry",
+           "save_q4_model"]

@@ -97,6 +97,22 @@ class ModelConfig:
             model_type=raw.get("model_type", ""),
         )
 
+    def to_dict(self) -> dict[str, Any]:
+        """HF config.json fields (from_dict(to_dict()) round-trips)."""
+        raw: dict[str, Any] = {k: getattr(self, k) for k in (
+            "architectures", "hidden_size", "intermediate_size", "num_hidden_layers",
+            "num_attention_heads", "num_key_value_heads", "head_dim", "vocab_size",
+            "max_position_embeddings", "rms_norm_eps", "rope_theta", "tie_word_embeddings",
+            "hidden_act", "torch_dtype", "bos_token_id", "eos_token_id", "attention_bias",
+            "model_type")}
+        if self.rope_scaling is not None:
+            r = self.rope_scaling
+            raw["rope_scaling"] = {"type": r.type, "factor": r.factor,
+                                   "low_freq_factor": r.low_freq_factor,
+                                   "high_freq_factor": r.high_freq_factor,
+                                   "original_max_position_embeddings": r.original_max_position_embeddings}
+        return raw
+
     @classmethod
     def qwen25_05b(cls) -> "ModelConfig":
         """Qwen2.5-0.5B geometry: 24 layers, hidden 896, 14 / 2 heads of 64,

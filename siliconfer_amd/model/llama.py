@@ -93,12 +93,16 @@ class LlamaModel:
     def __init__(self, config: ModelConfig, layers: list[LayerWeights], embed: torch.Tensor,
                  norm_w: torch.Tensor, group_size: int, max_seq: int,
                  act_dtype: torch.dtype = torch.float32, max_prefill: int = 512,
-                 fuse: bool = True):
-        if embed.dtype != torch.bfloat16:
-            raise SFError("the tied embedding must be bf16")
+                 fuse: bool = True, lm_head: torch.Tensor | None = None):
+        if embed.dtype != torch.bfloat16 or (lm_head is not None and lm_head.dtype != torch.bfloat16):
+            raise SFError("the embedding and the lm_head must be bf16")
+        if lm_head is not None and tuple(lm_head.shape) != tuple(embed.shape):
+            raise SFError("lm_head shape mismatch")
         if act_dtype not in _DT:
             raise SFError("act_dtype must be float32, float16 or bfloat16")
         self.config, self.layers, self.embed, self.norm_w = config, layers, embed, norm_w
+        # logits table: the tied embedding (llama.py:77-79 `as_linear`) or lm_head.weight
+        self.head = embed if lm_head is None else lm_head
         self.group_size, self.max_seq, self.act_dtype = group_size, max_seq, act_dtype
         self.max_prefill = max_prefill
         # decode folds each RMSNorm and the SwiGLU into the next projection
@@ -188,20 +192,25 @@ class LlamaModel:
         (fp16 scales as stored), biases, norms, the embedding as fp32."""
         out = {"embed": self.embed.float().cpu().numpy(), "norm": self.norm_w.cpu().numpy(),
                "layers": []}
+        if self.head is not self.embed:
+            out["lm_head"] = self.head.float().cpu().numpy()
         for L in self.layers:
             d = {}
             for name in ("qkv", "o", "gate_up", "down"):
                 w: Q4Weight = getattr(L, name)
-                pk, s, _ = w.canonical()
+                pk, s, z = w.canonical()
                 pk = pk.cpu().numpy()
                 s = s.float().cpu().numpy()
                 lo = (pk & 0x0F).astype(np.int16)
                 hi = (pk >> 4).astype(np.int16)
                 q = np.empty((pk.shape[0], pk.shape[1] * 2), np.int16)
                 q[:, 0::2], q[:, 1::2] = lo, hi
-                q = np.where(q > 7, q - 16, q).astype(np.float32)
                 g = self.group_size
-                d[name] = (q.reshape(q.shape[0], -1, g) * s[..., None]).reshape(q.shape)
+                if z is None:  # two's-complement codes
+                    q = np.where(q > 7, q - 16, q).astype(np.float32).reshape(q.shape[0], -1, g)
+                else:          # unsigned codes minus the group's zero-point
+                    q = q.astype(np.float32).reshape(q.shape[0], -1, g) - z.cpu().numpy()[..., None]
+                d[name] = (q * s[..., None]).reshape(pk.shape[0], -1)
             d["qkv_bias"] = None if L.qkv_bias is None else L.qkv_bias.cpu().numpy()
             d["w_in"], d["w_post"] = L.w_in.cpu().numpy(), L.w_post.cpu().numpy()
             out["layers"].append(d)
@@ -254,7 +263,7 @@ class LlamaModel:
 
     def _lm_head_norm(self, h_row, token, pos_inc, logits=True):
         self._chk(self.lib.sf_lm_head_argmax_rmsnorm(
-            self.embed.data_ptr(), h_row.data_ptr(), self.norm_w.data_ptr(),
+            self.head.data_ptr(), h_row.data_ptr(), self.norm_w.data_ptr(),
             float(self.config.rms_norm_eps), _DT[self.act_dtype],
             self.logits.data_ptr() if logits else None, self.V, self.H, token.data_ptr(), pos_inc,
             self.hist.data_ptr() if pos_inc else None, self.head_ws.data_ptr(), self.head_ws.numel(),
@@ -262,7 +271,7 @@ class LlamaModel:
 
     def _lm_head(self, x_row, token, pos_inc, logits=True):
         self._chk(self.lib.sf_lm_head_argmax(
-            self.embed.data_ptr(), x_row.data_ptr(), _DT[x_row.dtype],
+            self.head.data_ptr(), x_row.data_ptr(), _DT[x_row.dtype],
             self.logits.data_ptr() if logits else None, self.V, self.H, token.data_ptr(),
             pos_inc, self.hist.data_ptr() if pos_inc else None, self.head_ws.data_ptr(),
             self.head_ws.numel(), self._st()), "sf_lm_head_argmax")
