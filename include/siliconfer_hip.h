@@ -220,6 +220,20 @@ int sf_lm_head_argmax_rmsnorm(const void *w, const float *h, const float *norm_w
                               int *pos_inc, int32_t *hist, void *workspace, size_t workspace_bytes,
                               void *stream);
 
+/* Logits and greedy tokens of B = 1..8 rows at once: the target model's
+ * verify of K+1 = B positions in greedy speculative decoding
+ * (/root/reference/siliconfer/engine/speculative.py:166-189, which takes the
+ * argmax of each verify row of `t_log`). x [B, H] (x_dtype); logits [B, V]
+ * fp32 or NULL; tokens_out[b] = argmax of row b (lowest index on ties). Each
+ * row's logits equal sf_lm_head_argmax's for that row alone, bit for bit.
+ * Needs B * H * sizeof(x element) <= 65536. The workspace
+ * (sf_lm_head_rows_workspace_bytes, 256-byte aligned) is zero-filled before
+ * its first use; each call leaves it so. */
+size_t sf_lm_head_rows_workspace_bytes(int V, int B);
+int sf_lm_head_argmax_rows(const void *w, const void *x, int x_dtype, float *logits, int V, int H,
+                           int B, int32_t *tokens_out, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,9 @@ _SIGS = {
                                  _c_sz, _c_p]),
     "sf_lm_head_argmax_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_f, _c_i, _c_p, _c_i, _c_i, _c_p,
                                          _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "sf_lm_head_rows_workspace_bytes": (_c_sz, [_c_i, _c_i]),
+    "sf_lm_head_argmax_rows": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz,
+                                      _c_p]),
 }
 
 _lock = threading.Lock()

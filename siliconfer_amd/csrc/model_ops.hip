@@ -15,6 +15,7 @@
 // Positions and the greedy token can live in device memory, so one decode
 // step is a fixed sequence of launches that a HIP graph replays token after
 // token with no host round trip.
+#include <type_traits>
 #include <math.h>
 
 #include "sf_common.h"
@@ -320,6 +321,153 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Logits and greedy tokens of B <= 8 rows at once (a speculative verify's K+1
+// positions): one pass over the bf16 table for all rows, x staged in LDS as
+// fp32 [B][H]. Each row's dot products are the same fma chains and DPP tree as
+// k_lm_head_argmax, so a row's logits equal the single-row kernel's bit for
+// bit; per-row (value, index) partials and a last-block fold per row. x stays
+// in its own type in LDS (fp16 / bf16 widen exactly when read).
+constexpr int kRowsMax = 8;
+constexpr size_t kRowsLdsBytes = 65536;  // B * H * sizeof(x element)
+
+template <int XDT>
+__global__ void __launch_bounds__(kThreads)
+k_lm_head_rows(const uint16_t *__restrict__ w, const void *__restrict__ x,
+               float *__restrict__ logits, int V, int H, int B, int32_t *__restrict__ tokens_out,
+               float *part_val, int *part_idx, unsigned *counter) {
+  using XS = std::conditional_t<XDT == SF_F32, float, uint16_t>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs_raw[];
+  XS *xs = (XS *)xs_raw;  // [B][H]
+  __shared__ float bv_s[kRowsMax][kThreads / 64];
+  __shared__ int bi_s[kRowsMax][kThreads / 64];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < B * H; i += kThreads) xs[i] = ((const XS *)x)[i];
+  __syncthreads();
+  const int nch = H >> 3;
+  const int n_waves = gridDim.x * (kThreads / 64);
+  const int gw = blockIdx.x * (kThreads / 64) + wave;
+  float best[kRowsMax];
+  int best_i[kRowsMax];
+#pragma unroll
+  for (int b = 0; b < kRowsMax; ++b) {
+    best[b] = -INFINITY;
+    best_i[b] = 0x7fffffff;
+  }
+  constexpr int RU = 4, CPL = 2;  // as k_lm_head_argmax
+  for (int r0 = gw; r0 < V; r0 += RU * n_waves) {
+    u32x4 c[RU][CPL];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int row = min(r0 + u * n_waves, V - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int ch = min(lane + 64 * j, nch - 1);
+        c[u][j] = *(const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int row = r0 + u * n_waves;
+      for (int b = 0; b < B; ++b) {
+        const XS *xb = xs + (size_t)b * H;
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const int ch = lane + 64 * j;
+          if (ch < nch) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t p = c[u][j][e];
+              a = fmaf(sf_bitcast<float>(p << 16), sf_load_as_f32<XDT>(xb, ch * 8 + 2 * e), a);
+              a = fmaf(sf_bitcast<float>(p & 0xffff0000u), sf_load_as_f32<XDT>(xb, ch * 8 + 2 * e + 1), a);
+            }
+          }
+        }
+        for (int ch = lane + 64 * CPL; ch < nch; ch += 64) {
+          const u32x4 qv = *(const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a = fmaf(sf_bitcast<float>(qv[e] << 16), sf_load_as_f32<XDT>(xb, ch * 8 + 2 * e), a);
+            a = fmaf(sf_bitcast<float>(qv[e] & 0xffff0000u), sf_load_as_f32<XDT>(xb, ch * 8 + 2 * e + 1), a);
+          }
+        }
+        a = sf_wave_sum(a);
+        if (row < V) {
+          if (lane == 0 && logits) logits[(size_t)b * V + row] = a;
+          // runtime b: select into the compile-time slots
+#pragma unroll
+          for (int k = 0; k < kRowsMax; ++k)
+            if (k == b && better(a, row, best[k], best_i[k])) {
+              best[k] = a;
+              best_i[k] = row;
+            }
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kRowsMax; ++k) {
+      bv_s[k][wave] = best[k];
+      bi_s[k][wave] = best_i[k];
+    }
+  }
+  __syncthreads();
+  if (tid < B) {
+    float bb = bv_s[tid][0];
+    int bi = bi_s[tid][0];
+    for (int k = 1; k < kThreads / 64; ++k)
+      if (better(bv_s[tid][k], bi_s[tid][k], bb, bi)) {
+        bb = bv_s[tid][k];
+        bi = bi_s[tid][k];
+      }
+    __hip_atomic_store((uint32_t *)(part_val + (size_t)tid * gridDim.x + blockIdx.x),
+                       sf_bitcast<uint32_t>(bb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(part_idx + (size_t)tid * gridDim.x + blockIdx.x, bi, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // the last block folds each row's partials: wave w takes rows w, w + 4
+  {
+    for (int b = wave; b < B; b += kThreads / 64) {
+      float bb = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int k = lane; k < (int)gridDim.x; k += 64) {
+        const float v = sf_bitcast<float>(__hip_atomic_load(
+            (const uint32_t *)(part_val + (size_t)b * gridDim.x + k), __ATOMIC_RELAXED,
+            __HIP_MEMORY_SCOPE_AGENT));
+        const int i = __hip_atomic_load(part_idx + (size_t)b * gridDim.x + k, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        if (better(v, i, bb, bi)) {
+          bb = v;
+          bi = i;
+        }
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bb, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (better(ov, oi, bb, bi)) {
+          bb = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) tokens_out[b] = bi == 0x7fffffff ? 0 : bi;
+    }
+  }
+  __syncthreads();
+  if (tid == 0)  // ready for the next call on this workspace
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -454,4 +602,44 @@ extern "C" int sf_lm_head_argmax_rmsnorm(const void *w, const float *h, const fl
   const int rc = lm_head_launch(w, h, act_dtype, norm_w, eps, logits, V, H, token_out, pos_inc,
                                 hist, workspace, workspace_bytes, stream);
   return rc ? rc : sf_check_launch("sf_lm_head_argmax_rmsnorm");
+}
+
+extern "C" size_t sf_lm_head_rows_workspace_bytes(int V, int B) {
+  (void)V;
+  if (B < 1 || B > kRowsMax) return 0;
+  // counter (256 B slot), then per row kHeadBlocks (value, index) partials
+  return 256 + (size_t)B * kHeadBlocks * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int sf_lm_head_argmax_rows(const void *w, const void *x, int x_dtype, float *logits,
+                                      int V, int H, int B, int32_t *tokens_out, void *workspace,
+                                      size_t workspace_bytes, void *stream) {
+  SF_REQUIRE(V > 0 && H > 0 && B >= 1 && B <= kRowsMax, SF_EINVAL,
+             "invalid lm_head rows shape V=%d H=%d B=%d (B must be 1..%d)", V, H, B, kRowsMax);
+  SF_REQUIRE(x_dtype >= SF_F32 && x_dtype <= SF_BF16, SF_EINVAL, "bad x dtype %d", x_dtype);
+  const size_t lds = (size_t)B * H * (x_dtype == SF_F32 ? 4 : 2);
+  SF_REQUIRE(H % 8 == 0 && lds <= kRowsLdsBytes, SF_EUNSUPPORTED,
+             "hidden=%d x rows=%d: need a multiple of 8 and the rows in %zu bytes", H, B,
+             kRowsLdsBytes);
+  SF_REQUIRE(w && x && tokens_out && workspace, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(workspace_bytes >= sf_lm_head_rows_workspace_bytes(V, B), SF_EINVAL,
+             "lm_head workspace too small: %zu < %zu", workspace_bytes,
+             sf_lm_head_rows_workspace_bytes(V, B));
+  SF_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)workspace & 255) == 0, SF_EINVAL,
+             "weights must be 16-byte and workspace 256-byte aligned");
+  unsigned *counter = (unsigned *)workspace;
+  float *pv = (float *)((char *)workspace + 256);
+  int *pi = (int *)(pv + (size_t)B * kHeadBlocks);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *wb = (const uint16_t *)w;
+  if (x_dtype == SF_F32)
+    k_lm_head_rows<SF_F32><<<kHeadBlocks, kThreads, lds, st>>>(wb, x, logits, V, H, B, tokens_out,
+                                                               pv, pi, counter);
+  else if (x_dtype == SF_F16)
+    k_lm_head_rows<SF_F16><<<kHeadBlocks, kThreads, lds, st>>>(wb, x, logits, V, H, B, tokens_out,
+                                                               pv, pi, counter);
+  else
+    k_lm_head_rows<SF_BF16><<<kHeadBlocks, kThreads, lds, st>>>(wb, x, logits, V, H, B, tokens_out,
+                                                                pv, pi, counter);
+  return sf_check_launch("sf_lm_head_argmax_rows");
 }

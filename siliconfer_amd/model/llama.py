@@ -90,6 +90,8 @@ class LlamaModel:
     """Batch-1 int4 decoder on one GPU. `max_seq` bounds prompt + generated
     tokens (the KV cache capacity and the RoPE table)."""
 
+    VERIFY_ROWS = 8  # rows of one lm_head pass in verify()
+
     def __init__(self, config: ModelConfig, layers: list[LayerWeights], embed: torch.Tensor,
                  norm_w: torch.Tensor, group_size: int, max_seq: int,
                  act_dtype: torch.dtype = torch.float32, max_prefill: int = 512,
@@ -143,6 +145,11 @@ class LlamaModel:
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)   # counters start at zero
         hw = self.lib.sf_lm_head_workspace_bytes(self.V)
         self.head_ws = torch.zeros(hw, dtype=torch.uint8, device=dev)
+        # verify rows (speculative decoding): greedy token and logits per row
+        self.vtok = torch.zeros((self.VERIFY_ROWS,), dtype=torch.int32, device=dev)
+        self.vlogits = torch.zeros((self.VERIFY_ROWS, self.V), dtype=f32, device=dev)
+        rw = self.lib.sf_lm_head_rows_workspace_bytes(self.V, self.VERIFY_ROWS)
+        self.rows_ws = torch.zeros(rw, dtype=torch.uint8, device=dev)
         self.pos = 0
         self.graph = None
         self._prefill_bufs = None
@@ -231,6 +238,15 @@ class LlamaModel:
 
     def _gemm(self, w: Q4Weight, X: torch.Tensor, Y32: torch.Tensor, bias: torch.Tensor | None):
         M = X.shape[0]
+        if M <= 8 and w.in_features <= 16384:
+            # up to 8 rows (a short chunk, a speculative verify): the batch GEMV
+            # streams the weights once for all rows
+            self._chk(self.lib.sf_q4_gemv(w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], None,
+                                          _lib.SF_F32, Y32.data_ptr(),
+                                          None if bias is None else bias.data_ptr(), _lib.SF_F32, M,
+                                          w.out_features, w.in_features, w.group_size,
+                                          int(w.has_zeros), self._st()), "sf_q4_gemv")
+            return
         need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features, w.group_size)
         if need and (self._gemm_ws is None or self._gemm_ws.numel() < need):
             self._gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
@@ -315,7 +331,45 @@ class LlamaModel:
             done += n
         return int(self.token.item())
 
-    def _prefill_chunk(self, ids: np.ndarray, want_logits: bool):
+    def set_position(self, n: int) -> None:
+        """Trim the KV cache to its first n positions — QuantizedKVCache.trim
+        (/root/reference/siliconfer/model/kv_cache.py:107-112) as speculative
+        decoding uses it (engine/speculative.py:29-41). The codes past n stay
+        in place and are overwritten by the next tokens."""
+        n = int(n)
+        if not 0 <= n <= self.pos:
+            raise SFError(f"cannot trim the cache to {n} positions (it holds {self.pos})")
+        self.pos = n
+        self.pos_dev.fill_(n)
+
+    def verify(self, ids, want_logits: bool = False) -> list[int]:
+        """Append the B tokens `ids` at positions pos..pos+B-1 in one forward
+        and return the greedy next token after each of them — the target's
+        verify pass of speculative decoding (engine/speculative.py:277-283,
+        `t_log = target(verify_ids)`, with the greedy pick of each row). For
+        B <= 8 every projection is one batch GEMV over the B rows, so a
+        verify streams the weights once, like one decode step. `want_logits`
+        keeps the rows' logits in `self.vlogits[:B]` (B <= 8)."""
+        ids = np.asarray(ids, dtype=np.int64).reshape(-1)
+        B = int(ids.size)
+        if B == 0:
+            raise SFError("empty verify batch")
+        if ids.min() < 0 or ids.max() >= self.V:
+            raise SFError("token id out of range")
+        if self.pos + B > self.max_seq:
+            raise SFError(f"verify of {B} tokens at position {self.pos} exceeds the cache capacity "
+                          f"{self.max_seq}")
+        if want_logits and B > self.VERIFY_ROWS:
+            raise SFError(f"verify logits are kept for at most {self.VERIFY_ROWS} rows")
+        out = []
+        done = 0
+        while done < B:
+            n = min(self.max_prefill, B - done)
+            out += self._prefill_chunk(ids[done:done + n], want_logits, rows_head=True)
+            done += n
+        return out
+
+    def _prefill_chunk(self, ids: np.ndarray, want_logits: bool, rows_head: bool = False):
         T = int(ids.size)
         b = self._bufs(T)
         Hb, Xn, QKV, Q, A, Dl, GU, ACT = (b[k][:T] for k in ("H", "Xn", "QKV", "Q", "A", "Dl", "GU", "ACT"))
@@ -340,9 +394,22 @@ class LlamaModel:
                       "sf_silu_mul")
             self._gemm(L.down, ACT, Dl, None)
         self._rmsnorm(Hb, Dl, self.norm_w, Xn, T)
-        self._lm_head(Xn[T - 1], self.token, None, logits=want_logits)
+        toks = None
+        if rows_head:  # every row's greedy token, 8 rows per lm_head pass
+            R = self.VERIFY_ROWS
+            for r0 in range(0, T, R):
+                nr = min(R, T - r0)
+                self._chk(lib.sf_lm_head_argmax_rows(
+                    self.head.data_ptr(), Xn[r0:r0 + nr].data_ptr(), _DT[Xn.dtype],
+                    self.vlogits.data_ptr() if want_logits else None, self.V, self.H, nr,
+                    self.vtok.data_ptr(), self.rows_ws.data_ptr(), self.rows_ws.numel(), st),
+                    "sf_lm_head_argmax_rows")
+                toks = (toks or []) + self.vtok[:nr].tolist()
+        else:
+            self._lm_head(Xn[T - 1], self.token, None, logits=want_logits)
         self.pos += T
         self.pos_dev.fill_(self.pos)
+        return toks
 
     # ---------------------------------------------------------------- decode
     def decode_step(self, logits: bool = False) -> None:

@@ -130,3 +130,20 @@ def test_fused_gemv_rejects_bad_op_and_missing_norm_weight():
     assert "null pointer" in _lib.last_error()
     assert lib.sf_q4_gemv_fused(*args(_lib.SF_PRE_SILU_MUL, None, K=100)) == -1
     assert "divisible by group_size" in _lib.last_error()
+
+
+def test_lm_head_rows_validation_and_sizes():
+    lib = _lib.load()
+    assert lib.sf_lm_head_rows_workspace_bytes(151936, 8) == 256 + 8 * 1024 * 8
+    assert lib.sf_lm_head_rows_workspace_bytes(1000, 9) == 0
+    w, x, tok, ws = 256 * 1024, 4096, 8192, 512 * 1024  # fake addresses: validation fails first
+    big = 1 << 20
+    args = lambda xdt, H, B, wsb=big: (w, x, xdt, None, 1000, H, B, tok, ws, wsb, None)
+    assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F16, 896, 0)) == -1
+    assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F16, 896, 9)) == -1
+    assert "must be 1..8" in _lib.last_error()
+    assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F32, 4096, 8)) == -2   # 128 KB of rows
+    assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F16, 900, 2)) == -2    # not a multiple of 8
+    assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F16, 896, 8, wsb=1024)) == -1
+    assert "workspace too small" in _lib.last_error()
+    assert lib.sf_lm_head_argmax_rows(*args(7, 896, 2)) == -1

@@ -71,8 +71,13 @@ def test_prefill_in_chunks_equals_one_prefill(dev):
     b = LlamaModel.random_init(SMALL, seed=13, device=dev, max_seq=64, max_prefill=5)
     ids = np.random.default_rng(14).integers(0, SMALL.vocab_size, 17)
     ta, tb = a.prefill(ids), b.prefill(ids)
-    assert_close(b.logits.cpu().numpy(), a.logits.cpu().numpy(), 1e-4, "chunked prefill")
-    assert ta == tb
+    # chunks of <= 8 rows run the batch GEMV, the 17-row prompt the GEMM: the
+    # two paths round differently, so an int8 KV code may differ by one step
+    # (the module docstring's 2e-3)
+    la = a.logits.cpu().numpy()
+    assert_close(b.logits.cpu().numpy(), la, 2e-3, "chunked prefill")
+    if margin_ok(la, 2e-3):
+        assert ta == tb
 
 
 def test_graph_replay_equals_eager(dev):
