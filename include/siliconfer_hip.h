@@ -167,6 +167,18 @@ int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes, cons
                          int out_dtype, int T_q, int H, int KVH, int T0, int T_cap, int D,
                          float scale, void *stream);
 
+/* The same causal attention with T0 in device memory (*T0_dev, read when the
+ * kernel runs): the verify rows of speculative decoding replayed from a HIP
+ * graph at a position the host does not know when it records the launch.
+ * n_splits (<= 0: sf_attn_default_splits(T_q, KVH, T_max)) and the workspace
+ * (sf_attn_workspace_bytes(T_q, H, D, n_splits), zero-filled before its first
+ * use) are fixed for T0 + T_q <= T_max; rows past T_cap see T_cap tokens. */
+int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                             const void *k_scales, const int8_t *v_codes, const void *v_scales,
+                             int scale_dtype, void *out, int out_dtype, void *workspace,
+                             size_t workspace_bytes, int T_q, int H, int KVH, const int *T0_dev,
+                             int T_max, int T_cap, int D, float scale, int n_splits, void *stream);
+
 /* ---- decoder step operations (model runner) -------------------------------
  * The per-token work of the reference's TransformerBlock / LlamaModel around
  * the projections (/root/reference/siliconfer/model/layers.py:14-163,

@@ -52,6 +52,9 @@ _SIGS = {
                                        _c_i, _c_f, _c_i, _c_p]),
     "sf_attn_prefill_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                     _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_p]),
+    "sf_attn_prefill_i8kv_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p,
+                                        _c_sz, _c_i, _c_i, _c_i, _c_p, _c_i, _c_i, _c_i, _c_f,
+                                        _c_i, _c_p]),
     "sf_embed": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p]),
     "sf_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_f, _c_p]),
     "sf_rope_kv_append": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p,

@@ -345,10 +345,11 @@ k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
   const bool dact = d0 < D;
   const int dq = dact ? d0 : 0;
   // Length: the host's T, or a device length plus T (decode steps replayed
-  // from a graph), or for a causal prefill T tokens before query row b plus
-  // the row itself; the cache then has batch 1.
+  // from a graph), or for a causal prefill T0 tokens before query row b plus
+  // the row itself (T0 = the host's T, or the device length); the cache then
+  // has batch 1.
   int Tv = T_dev ? *T_dev + T : T;
-  if (causal) Tv = T + b + 1;
+  if (causal) Tv = (T_dev ? *T_dev : T) + b + 1;
   Tv = max(0, min(Tv, T_cap));
   const int tile = (Tv + n_splits - 1) / n_splits;
   const int t0 = split * tile, t1 = min(t0 + tile, Tv);
@@ -624,7 +625,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane & 15, g = lane >> 4;
   int Tv = T_dev ? *T_dev + T : T;
-  if (causal) Tv = T + b + 1;
+  if (causal) Tv = (T_dev ? *T_dev : T) + b + 1;
   Tv = max(0, min(Tv, T_cap));
   const int tile = ((Tv + n_splits - 1) / n_splits + 31) & ~31;
   const int t0 = min(split * tile, Tv), t1 = min(t0 + tile, Tv);
@@ -1099,4 +1100,21 @@ extern "C" int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_
   return attn_launch("sf_attn_prefill_i8kv", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, nullptr, 0, T_q, H, KVH, T0, nullptr, 1, T_cap, D,
                      scale, 1, stream);
+}
+
+extern "C" int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                                        const void *k_scales, const int8_t *v_codes,
+                                        const void *v_scales, int scale_dtype, void *out,
+                                        int out_dtype, void *workspace, size_t workspace_bytes,
+                                        int T_q, int H, int KVH, const int *T0_dev, int T_max,
+                                        int T_cap, int D, float scale, int n_splits,
+                                        void *stream) {
+  SF_REQUIRE(T_q > 0 && H > 0 && KVH > 0 && D > 0 && T_max >= T_q && T_max <= T_cap, SF_EINVAL,
+             "invalid prefill attention shape T_q=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", T_q, H,
+             KVH, T_max, T_cap, D);
+  SF_REQUIRE(T0_dev, SF_EINVAL, "null pointer argument");
+  if (n_splits <= 0) n_splits = sf_attn_default_splits(T_q, KVH, T_max);
+  return attn_launch("sf_attn_prefill_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
+                     scale_dtype, out, out_dtype, workspace, workspace_bytes, T_q, H, KVH, 0,
+                     T0_dev, 1, T_cap, D, scale, n_splits, stream);
 }

@@ -7,7 +7,8 @@ Each round (speculative.py:259-352):
      steps, replayed from the draft's HIP graph without a host round trip;
   2. the target verifies [cur, d_0 .. d_{K-1}] in one forward
      (`LlamaModel.verify`: K + 1 <= 8 rows run every projection as one batch
-     GEMV, so the verify streams the target's weights once);
+     GEMV, so the verify streams the target's weights once; it replays the
+     target's verify graph for K + 1 rows, recorded on first use);
   3. d_q is accepted while it equals the target's greedy token after row q
      (`_tok_prob` at temperature 0 gives 1 or 0, :44-51); the first mismatch
      is replaced by the target's token, and a fully accepted round adds the
@@ -102,6 +103,11 @@ def speculative_generate(draft, target, prompt_ids, max_tokens: int = 128, K: in
             raise SFError(f"the {name} cache holds {m.max_seq} positions; prompt + max_tokens + "
                           f"K_max + 1 = {need}")
     dev = torch.device(target.device)
+    # one verify graph per batch K+1 the rounds can use (recorded once)
+    sizes = {k + 1 for k in range(K_min, K_max + 1) if k + 1 <= 8}
+    missing = sorted(sizes - target.verify_graph_sizes)
+    if missing:
+        target.capture_verify(missing)
 
     def sync():
         if dev.type == "cuda":

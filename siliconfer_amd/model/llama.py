@@ -152,6 +152,8 @@ class LlamaModel:
         self.rows_ws = torch.zeros(rw, dtype=torch.uint8, device=dev)
         self.pos = 0
         self.graph = None
+        self._verify_graphs = {}
+        self._vbufs = None
         self._prefill_bufs = None
         self._gemm_ws = None
 
@@ -300,18 +302,20 @@ class LlamaModel:
 
     def _bufs(self, T):
         if self._prefill_bufs is None or self._prefill_bufs["T"] < T:
-            dev, a, f32 = self.device, self.act_dtype, torch.float32
-            self._prefill_bufs = dict(
-                T=T, H=torch.empty((T, self.H), dtype=f32, device=dev),
-                Xn=torch.empty((T, self.H), dtype=a, device=dev),
-                QKV=torch.empty((T, self.qkv_n), dtype=f32, device=dev),
-                Q=torch.empty((T, self.Hq, self.D), dtype=a, device=dev),
-                A=torch.empty((T, self.Hq * self.D), dtype=a, device=dev),
-                Dl=torch.empty((T, self.H), dtype=f32, device=dev),
-                GU=torch.empty((T, 2 * self.I), dtype=f32, device=dev),
-                ACT=torch.empty((T, self.I), dtype=a, device=dev),
-                ids=torch.empty((T,), dtype=torch.int32, device=dev))
+            self._prefill_bufs = self._alloc_rows(T)
         return self._prefill_bufs
+
+    def _alloc_rows(self, T):
+        dev, a, f32 = self.device, self.act_dtype, torch.float32
+        return dict(T=T, H=torch.empty((T, self.H), dtype=f32, device=dev),
+                    Xn=torch.empty((T, self.H), dtype=a, device=dev),
+                    QKV=torch.empty((T, self.qkv_n), dtype=f32, device=dev),
+                    Q=torch.empty((T, self.Hq, self.D), dtype=a, device=dev),
+                    A=torch.empty((T, self.Hq * self.D), dtype=a, device=dev),
+                    Dl=torch.empty((T, self.H), dtype=f32, device=dev),
+                    GU=torch.empty((T, 2 * self.I), dtype=f32, device=dev),
+                    ACT=torch.empty((T, self.I), dtype=a, device=dev),
+                    ids=torch.empty((T,), dtype=torch.int32, device=dev))
 
     def prefill(self, ids, want_logits: bool = True) -> int:
         """Run the prompt (appending to the cache) and return the greedy next
@@ -348,8 +352,9 @@ class LlamaModel:
         verify pass of speculative decoding (engine/speculative.py:277-283,
         `t_log = target(verify_ids)`, with the greedy pick of each row). For
         B <= 8 every projection is one batch GEMV over the B rows, so a
-        verify streams the weights once, like one decode step. `want_logits`
-        keeps the rows' logits in `self.vlogits[:B]` (B <= 8)."""
+        verify streams the weights once, like one decode step, and after
+        `capture_verify()` it is one graph replay. `want_logits` keeps the
+        rows' logits in `self.vlogits[:B]` (B <= 8)."""
         ids = np.asarray(ids, dtype=np.int64).reshape(-1)
         B = int(ids.size)
         if B == 0:
@@ -361,6 +366,13 @@ class LlamaModel:
                           f"{self.max_seq}")
         if want_logits and B > self.VERIFY_ROWS:
             raise SFError(f"verify logits are kept for at most {self.VERIFY_ROWS} rows")
+        g = self._verify_graphs.get(B) if not want_logits else None
+        if g is not None:
+            self._vids_host[:B].copy_(torch.from_numpy(ids.astype(np.int32)))
+            self._vbufs["ids"][:B].copy_(self._vids_host[:B], non_blocking=True)
+            g.replay()
+            self.pos += B  # the graph advanced pos_dev
+            return self.vtok[:B].tolist()
         out = []
         done = 0
         while done < B:
@@ -369,24 +381,85 @@ class LlamaModel:
             done += n
         return out
 
+    @property
+    def verify_graph_sizes(self) -> set[int]:
+        return set(self._verify_graphs)
+
+    def capture_verify(self, sizes=range(1, 9)) -> None:
+        """Record verify() of B rows as one HIP graph per B in `sizes` (B <=
+        8): ids come from a fixed device buffer, positions from pos_dev (the
+        graph advances it by B), tokens land in `self.vtok`. Verifies that
+        ask for logits still run eagerly."""
+        if self._vbufs is None:
+            R = self.VERIFY_ROWS
+            self._vbufs = self._alloc_rows(R)
+            self._vids_host = torch.zeros((R,), dtype=torch.int32).pin_memory()
+            wb = self.lib.sf_attn_workspace_bytes(R, self.Hq, self.D, self.attn_splits)
+            self._vattn_ws = torch.zeros(max(wb, 256), dtype=torch.uint8, device=self.device)
+        for B in sizes:
+            if not 1 <= B <= self.VERIFY_ROWS:
+                raise SFError(f"verify graphs hold 1..{self.VERIFY_ROWS} rows")
+            torch.cuda.synchronize(self.device)
+            s = torch.cuda.Stream(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                self._rows_forward(self._vbufs, B, True)
+                self._rows_head(self._vbufs["Xn"][:B], B, False)
+                self.pos_dev.add_(B)
+            torch.cuda.synchronize(self.device)
+            self._verify_graphs[B] = g
+
     def _prefill_chunk(self, ids: np.ndarray, want_logits: bool, rows_head: bool = False):
         T = int(ids.size)
         b = self._bufs(T)
+        b["ids"][:T].copy_(torch.from_numpy(ids.astype(np.int32)))
+        self._rows_forward(b, T, False)
+        Xn = b["Xn"][:T]
+        toks = None
+        if rows_head:  # every row's greedy token, 8 rows per lm_head pass
+            R = self.VERIFY_ROWS
+            toks = []
+            for r0 in range(0, T, R):
+                nr = min(R, T - r0)
+                self._rows_head(Xn[r0:r0 + nr], nr, want_logits)
+                toks += self.vtok[:nr].tolist()
+        else:
+            self._lm_head(Xn[T - 1], self.token, None, logits=want_logits)
+        self.pos += T
+        self.pos_dev.fill_(self.pos)
+        return toks
+
+    def _rows_head(self, Xn, nr, want_logits):
+        self._chk(self.lib.sf_lm_head_argmax_rows(
+            self.head.data_ptr(), Xn.data_ptr(), _DT[Xn.dtype],
+            self.vlogits.data_ptr() if want_logits else None, self.V, self.H, nr,
+            self.vtok.data_ptr(), self.rows_ws.data_ptr(), self.rows_ws.numel(), self._st()),
+            "sf_lm_head_argmax_rows")
+
+    def _rows_forward(self, b, T, dev_pos: bool):
+        """Embed b["ids"][:T], run every layer over the T rows at positions
+        pos.. (host `self.pos`, or pos_dev when dev_pos: graph-replayable) and
+        leave the final-normed rows in b["Xn"][:T]."""
         Hb, Xn, QKV, Q, A, Dl, GU, ACT = (b[k][:T] for k in ("H", "Xn", "QKV", "Q", "A", "Dl", "GU", "ACT"))
-        idt = b["ids"][:T]
-        idt.copy_(torch.from_numpy(ids.astype(np.int32)))
         lib, st = self.lib, self._st()
-        self._chk(lib.sf_embed(idt.data_ptr(), self.embed.data_ptr(), _lib.SF_BF16, Hb.data_ptr(), T,
-                               self.H, self.V, st), "sf_embed")
+        self._chk(lib.sf_embed(b["ids"].data_ptr(), self.embed.data_ptr(), _lib.SF_BF16, Hb.data_ptr(),
+                               T, self.H, self.V, st), "sf_embed")
+        pos_dev = self.pos_dev.data_ptr() if dev_pos else None
         for l, L in enumerate(self.layers):
             self._rmsnorm(Hb, None if l == 0 else Dl, L.w_in, Xn, T)
             self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
-            self._rope_append(l, QKV, Q, T, None, self.pos)
-            self._chk(lib.sf_attn_prefill_i8kv(
-                Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
-                self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, A.data_ptr(),
-                _DT[A.dtype], T, self.Hq, self.KVH, self.pos, self.max_seq, self.D, self.scale, st),
-                "sf_attn_prefill_i8kv")
+            self._rope_append(l, QKV, Q, T, pos_dev, 0 if dev_pos else self.pos)
+            args = (Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
+                    self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, A.data_ptr(),
+                    _DT[A.dtype])
+            if dev_pos:
+                self._chk(lib.sf_attn_prefill_i8kv_dev(
+                    *args, self._vattn_ws.data_ptr(), self._vattn_ws.numel(), T, self.Hq, self.KVH,
+                    pos_dev, self.max_seq, self.max_seq, self.D, self.scale, self.attn_splits, st),
+                    "sf_attn_prefill_i8kv_dev")
+            else:
+                self._chk(lib.sf_attn_prefill_i8kv(*args, T, self.Hq, self.KVH, self.pos, self.max_seq,
+                                                   self.D, self.scale, st), "sf_attn_prefill_i8kv")
             self._gemm(L.o, A, Dl, None)
             self._rmsnorm(Hb, Dl, L.w_post, Xn, T)
             self._gemm(L.gate_up, Xn, GU, None)
@@ -394,22 +467,6 @@ class LlamaModel:
                       "sf_silu_mul")
             self._gemm(L.down, ACT, Dl, None)
         self._rmsnorm(Hb, Dl, self.norm_w, Xn, T)
-        toks = None
-        if rows_head:  # every row's greedy token, 8 rows per lm_head pass
-            R = self.VERIFY_ROWS
-            for r0 in range(0, T, R):
-                nr = min(R, T - r0)
-                self._chk(lib.sf_lm_head_argmax_rows(
-                    self.head.data_ptr(), Xn[r0:r0 + nr].data_ptr(), _DT[Xn.dtype],
-                    self.vlogits.data_ptr() if want_logits else None, self.V, self.H, nr,
-                    self.vtok.data_ptr(), self.rows_ws.data_ptr(), self.rows_ws.numel(), st),
-                    "sf_lm_head_argmax_rows")
-                toks = (toks or []) + self.vtok[:nr].tolist()
-        else:
-            self._lm_head(Xn[T - 1], self.token, None, logits=want_logits)
-        self.pos += T
-        self.pos_dev.fill_(self.pos)
-        return toks
 
     # ---------------------------------------------------------------- decode
     def decode_step(self, logits: bool = False) -> None:

@@ -133,6 +133,44 @@ def test_verify_rows_match_decode_and_oracle(dev, act, B):
             assert near_tie(ref[r], toks[r], OM.greedy(ref[r]), tol), f"row {r}: token"
 
 
+@pytest.mark.parametrize("max_seq,prompt_len", [(64, 9), (2048, 1100)])
+def test_verify_graph_equals_eager(dev, max_seq, prompt_len):
+    """verify() replayed from its graph (positions read on the device) gives
+    the eager verify's tokens and cache; at max_seq > 1024 the graph's causal
+    attention runs split (the eager one is single-split), so tokens are
+    compared up to near-ties and only the first layer's cache (written before
+    any attention) bit for bit."""
+    ms = [LlamaModel.random_init(SMALL, seed=45, group_size=64, device=dev, max_seq=max_seq,
+                                 act_dtype=torch.float16) for _ in range(2)]
+    g, e = ms
+    g.capture_verify()
+    assert g.verify_graph_sizes == set(range(1, 9))
+    rng = np.random.default_rng(46)
+    prompt = rng.integers(0, SMALL.vocab_size, prompt_len)
+    for m in ms:
+        m.reset()
+        m.prefill(prompt)
+    for B in (1, 3, 8, 2):
+        feed = rng.integers(0, SMALL.vocab_size, B)
+        tg = g.verify(feed)
+        te = e.verify(feed, want_logits=True)
+        assert g.pos == e.pos and int(g.pos_dev.item()) == g.pos
+        if max_seq <= 1024:
+            assert tg == te
+        else:
+            lg = e.vlogits[:B].cpu().numpy()
+            for r in range(B):
+                if tg[r] != te[r]:
+                    assert near_tie(lg[r], tg[r], te[r], 1e-2), f"B={B} row {r}"
+        n = g.pos
+        for l in range(SMALL.num_hidden_layers if max_seq <= 1024 else 1):
+            assert torch.equal(g.k_codes[l][:, :n], e.k_codes[l][:, :n])
+            assert torch.equal(g.v_scales[l][:, :n], e.v_scales[l][:, :n])
+        # trim back one row each time: the next verify overwrites it
+        g.set_position(n - 1)
+        e.set_position(n - 1)
+
+
 def test_trim_discards_stale_rows(dev):
     """After set_position(n) the cache behaves as if it held only n tokens:
     two runs whose first verify differs only in the rows past n give

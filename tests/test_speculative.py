@@ -44,6 +44,7 @@ class FakeDecoder:
         self.hist = torch.zeros(max_seq + 1, dtype=torch.int32)
         self.pos = 0
         self.calls = []
+        self.verify_graph_sizes = set(range(1, 9))
 
     def reset(self):
         self.pos = 0
