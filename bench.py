@@ -328,6 +328,92 @@ def e2e_decode(dev, runs: int = 3):
     return out
 
 
+SPEC_DRAFT = dict(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                  num_attention_heads=4, num_key_value_heads=2, head_dim=64)
+
+
+def spec_draft(dev, cfg, act):
+    """A 2-layer draft with the target's vocabulary (random weights)."""
+    from siliconfer_amd.model.config import ModelConfig
+    from siliconfer_amd.model.llama import LlamaModel
+
+    dcfg = ModelConfig(vocab_size=cfg.vocab_size, rms_norm_eps=cfg.rms_norm_eps,
+                       rope_theta=cfg.rope_theta, tie_word_embeddings=True, **SPEC_DRAFT)
+    return LlamaModel.random_init(dcfg, seed=5, group_size=64, device=dev,
+                                  max_seq=E2E_PROMPT + E2E_TOKENS + 256, act_dtype=act)
+
+
+def e2e_speculative(dev, reps: int = 20):
+    """Config-5 target (fp16 activations) after the 512-token prompt: device
+    time of one verify of B = K+1 rows (its HIP graph replayed between HIP
+    events, the position reset by a one-element fill each time) against one
+    decode step, and greedy speculative generation of 256 tokens with a
+    2-layer random draft (tok/s, acceptance). Random weights make greedy
+    text repetitive, so the acceptance rate here says nothing about a real
+    draft; the verify / decode cost ratio is the figure that carries over."""
+    import torch
+
+    from siliconfer_amd.engine import speculative_generate
+
+    cfg, t, ids = e2e_model(dev, torch.float16)
+    t.capture()
+    t.capture_verify()
+    t.reset()
+    t.prefill(ids)
+    N = t.pos
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def dev_ms(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def one_verify(B):
+        t.pos_dev.fill_(N)
+        t._verify_graphs[B].replay()
+
+    def one_decode():
+        t.pos_dev.fill_(N)
+        t.graph.replay()
+
+    decode_ms = dev_ms(one_decode)
+    verify = {B: round(dev_ms(lambda: one_verify(B)), 4) for B in (1, 2, 4, 8)}
+    t.set_position(N)
+    draft = spec_draft(dev, cfg, torch.float16)
+    draft.capture()
+    out = {"decode_step_ms": round(decode_ms, 4), "verify_ms": verify,
+           "verify8_over_decode": round(verify[8] / decode_ms, 3)}
+    for K in (3, 7):
+        speculative_generate(draft, t, ids, max_tokens=32, K=K)
+        r = speculative_generate(draft, t, ids, max_tokens=E2E_TOKENS, K=K)
+        out[f"K{K}"] = {"tok_s": round(r.effective_tok_s, 1),
+                        "acceptance": round(r.acceptance_rate, 3), "rounds": r.total_rounds}
+    return out
+
+
+def profile_verify(dev, reps: int = 8):
+    """Kernel-trace workload: config-5 prompt, then `reps` replays of the
+    8-row verify graph (the position reset before each)."""
+    import torch
+
+    _, t, ids = e2e_model(dev, torch.float16)
+    t.capture_verify([8])
+    t.reset()
+    t.prefill(ids)
+    N = t.pos
+    for _ in range(reps):
+        t.pos_dev.fill_(N)
+        t._verify_graphs[8].replay()
+    torch.cuda.synchronize()
+
+
 def e2e_cpu_baseline(dev, budget_s: float):
     """The numpy restatement of the forward pass (oracle/model.py) on the host
     cores, same weights: a 512-token prompt, then decode steps for about
@@ -567,6 +653,9 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end decode")
     ap.add_argument("--profile-e2e", action="store_true",
                     help="only run eager config-5 decode steps (for rocprofv3)")
+    ap.add_argument("--profile-verify", action="store_true",
+                    help="only run config-5 8-row verify graph replays (for rocprofv3)")
+    ap.add_argument("--no-spec", action="store_true", help="skip the speculative-decoding leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of reference CPU work")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -600,6 +689,10 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.profile_kernels:
         profile_kernels(dev)
+        return 0
+    if args.profile_verify:
+        profile_verify(dev)
+        print(json.dumps({"profile_verify": "prefill 512 + 8 replays of the 8-row verify graph"}))
         return 0
     if args.profile_e2e:
         _, m, ids = e2e_model(dev, torch.float16)
@@ -640,6 +733,7 @@ def main() -> int:
     e2e = None if args.no_e2e else e2e_decode(dev)
     if e2e is not None and not args.no_cpu:
         e2e["cpu_baseline"] = e2e_cpu_baseline(dev, args.cpu_budget)
+    spec = None if (args.no_e2e or args.no_spec) else e2e_speculative(dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
 
     line = {
@@ -676,6 +770,7 @@ def main() -> int:
         "cases": cases,
         "decode_tok_s": None if e2e is None else e2e["fp16"]["decode_tok_s"],
         "e2e_config5": e2e,
+        "speculative_config5": spec,
         "secondary": sec,
         "cpu_baseline": cpu,
     }
