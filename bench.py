@@ -532,9 +532,10 @@ def _short_kernel(name: str) -> str:
         pre = {None: "", "0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(6)]
         return (f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},"
                 f"x={m.group(5)}{pre}>")
-    m = re.search(r"k_q4_gemv_mfmaILi(\d+)ELb(\d)ELi(\d+)", name)
+    m = re.search(r"k_q4_gemv_mfmaILi(\d+)ELb(\d)ELi(\d+)E(?:Li(\d+))?", name)
     if m:
-        return f"k_q4_gemv_mfma<LW={m.group(1)},asym={m.group(2)},BPW={m.group(3)}>"
+        t = f",T={m.group(4)}" if m.group(4) else ""
+        return f"k_q4_gemv_mfma<LW={m.group(1)},asym={m.group(2)},BPW={m.group(3)}{t}>"
     m = re.search(r"(k_[a-z0-9_]+|__amd_rocclr_[A-Za-z]+|at::native::[a-z_]+)", name)
     return m.group(1) if m else name[:40]
 

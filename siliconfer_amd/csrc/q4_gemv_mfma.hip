@@ -9,8 +9,14 @@
 // weight is dequantized once to an exact fp16 integer (q - z), and a lane needs
 // 16 bytes of activations per MFMA.
 //
-// Layout: one workgroup per 16 weight rows; wave w covers the K blocks
-// [w * BPW, (w + 1) * BPW). A block is one scale group: lane l (row
+// Layout: one workgroup per T x 16 weight rows (T row tiles per wave, 1 or
+// 4); wave w covers the K blocks [w * BPW, (w + 1) * BPW) of every tile, so
+// each activation fragment it loads feeds T MFMAs. Every workgroup reads the
+// activations of the whole K from L2 (they do not stay in L1), so on wide
+// matrices four tiles per wave cut that stream, which the L1/address path
+// otherwise spends most of its cycles on (measured with TA/TCP counters),
+// four times. Lanes of A rows >= B load nothing (a buffer load past the
+// resource's end returns zero). A block is one scale group: lane l (row
 // n = l % 16, k-group kg = l / 16) loads LW bytes of row n per block, LW = 16
 // for group size 128 (four MFMAs per load) and 8 for group size 64 (two). The
 // wider load halves the cache lines a wave instruction touches per byte: the
@@ -36,7 +42,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTileN = 16;
-constexpr int kMaxWaves = 8;
+constexpr int kMaxWaves = 16;
 
 // Per-lane weight load width LW (bytes): 16 when a group spans 128 k, else 8.
 // A block is the K a wave instruction covers: 16 rows x (4 lanes x LW bytes),
@@ -45,8 +51,14 @@ template <int LW> struct WLoad;
 template <> struct WLoad<8> { typedef u32x2 T; static constexpr int kMaxBpw = 24; };
 template <> struct WLoad<16> { typedef u32x4 T; static constexpr int kMaxBpw = 12; };
 
-template <int LW, bool ASYM, int BPW>
-__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 3)))
+// Waves per workgroup a variant may use: 16 where its registers fit the
+// 128-VGPR budget of a 1024-thread workgroup, else 8 (256 VGPRs).
+__host__ __device__ constexpr int mfma_max_waves(int LW, bool asym, int bpw, int T) {
+  return (T > 1 || bpw * LW <= (asym ? 64 : 128)) ? 16 : 8;
+}
+
+template <int LW, bool ASYM, int BPW, int T>
+__global__ void __launch_bounds__(mfma_max_waves(LW, ASYM, BPW, T) * 64)
 k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
                const uint8_t *__restrict__ ztile, const f16 *__restrict__ x, void *__restrict__ y,
                int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt, int B,
@@ -58,67 +70,83 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
   constexpr int XR = BPW * NM <= 16 ? BPW : 16 / NM;
   constexpr int XPRE = XR == BPW ? BPW : XR - 1;
   typedef typename WLoad<LW>::T wvec_t;
-  __shared__ float red[kMaxWaves][8][kTileN];
+  __shared__ float red[kMaxWaves][8][T * kTileN];
 
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nl = lane & 15, kg = lane >> 4;
-  const int n0 = blockIdx.x * kTileN;
-  const int n = min(n0 + nl, N - 1);  // rows past N re-read row N-1; never stored
+  const int n0 = blockIdx.x * T * kTileN;
+  int nt[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) nt[t] = min(n0 + t * kTileN + nl, N - 1);  // rows past N re-read row N-1
   const int blk0 = wave * BPW;        // the host launches only waves with blk0 < nblk
   const int cnt = min(BPW, nblk - blk0);
   const int blast = blk0 + cnt - 1;   // blocks past the wave's own re-read its last one
   const int Kh = K >> 1;
 
   // lane (row n, k-group kg) covers k = KB blk + 2 LW kg .. + 2 LW - 1 of each block
-  const f16 *xr = x + (size_t)min(nl, B - 1) * K + kg * 2 * LW;
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, B * K * 2, 0x00020000);
+  const int xoff = nl < B ? (nl * K + kg * 2 * LW) * 2 : 0x40000000;
   u32x4 xs[XR][NM];
   auto xload = [&](int i) {
-    const u32x4 *xq = (const u32x4 *)(xr + (size_t)min(blk0 + i, blast) * KB);
+    const int o = xoff + min(blk0 + i, blast) * KB * 2;
 #pragma unroll
-    for (int j = 0; j < NM; ++j) xs[i % XR][j] = xq[j];
+    for (int j = 0; j < NM; ++j) xs[i % XR][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, o + j * 16, 0, 0);
   };
 #pragma unroll
   for (int i = 0; i < XPRE; ++i) xload(i);
 
-  uint32_t sbits[BPW], zbits[BPW];  // one group per block
-  {
-    const size_t cell0 = (size_t)(n >> 3) * G;
+  uint32_t sbits[T][BPW], zbits[T][BPW];  // one group per block
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const size_t cell0 = (size_t)(nt[t] >> 3) * G;
 #pragma unroll
     for (int q = 0; q < BPW; ++q) {
       const size_t cell = cell0 + min(blk0 + q, G - 1);
-      sbits[q] = ((const uint16_t *)stile)[cell * 8 + (n & 7)];
-      if constexpr (ASYM) zbits[q] = ztile[cell * 4 + ((n & 7) >> 1)];
+      sbits[t][q] = ((const uint16_t *)stile)[cell * 8 + (nt[t] & 7)];
+      if constexpr (ASYM) zbits[t][q] = ztile[cell * 4 + ((nt[t] & 7) >> 1)];
     }
   }
 
-  wvec_t wv[BPW];
-  const uint8_t *wrow = w + (size_t)n * Kh + kg * LW;
+  wvec_t wv[T][BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i)
-    wv[i] = __builtin_nontemporal_load((const wvec_t *)(wrow + (size_t)min(blk0 + i, blast) * 4 * LW));
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      wv[t][i] = __builtin_nontemporal_load((const wvec_t *)(w + (size_t)nt[t] * Kh + kg * LW +
+                                                             (size_t)min(blk0 + i, blast) * 4 * LW));
   // keep every load above issued before any math (the scheduler would otherwise
   // interleave them with the MFMAs to save registers)
   __builtin_amdgcn_sched_barrier(0);
 
   const half2_t sixteenth = {(f16)0.0625f, (f16)0.0625f};
   const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  float4_t part = zero4;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // C rows b = 4 kg + r, column n
+  float4_t part[T];
+  float acc[T][4];  // C rows b = 4 kg + r, column n
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    part[t] = zero4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     if (i + XPRE < BPW) xload(i + XPRE);
     // blocks i >= cnt (only in a workgroup's last wave) are computed on re-read
     // data and dropped at the scale step by a select: a branch here would let
     // the compiler sink this block's loads into it, after the wait
-    uint32_t z = 8u;  // offset-binary symmetric codes
-    if constexpr (ASYM) {
-      uint32_t zb = zbits[i];
-      asm volatile("" : "+v"(zb));  // use the loaded bits here, not right after the load
-      z = (zb >> (4 * (n & 1))) & 15u;
+    half2_t c1[T], c2[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t z = 8u;  // offset-binary symmetric codes
+      if constexpr (ASYM) {
+        uint32_t zb = zbits[t][i];
+        asm volatile("" : "+v"(zb));  // use the loaded bits here, not right after the load
+        z = (zb >> (4 * (nt[t] & 1))) & 15u;
+      }
+      c1[t] = sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);        // -(1024 + z)
+      c2[t] = sf_bitcast<half2_t>((0xD400u + 16u * z) * 0x10001u);  // -(64 + z)
     }
-    const half2_t c1 = sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);        // -(1024 + z)
-    const half2_t c2 = sf_bitcast<half2_t>((0xD400u + 16u * z) * 0x10001u);  // -(64 + z)
 #pragma unroll
     for (int j = 0; j < NM; ++j) {
       // A: x[k0, k4, k1, k5, k2, k6, k3, k7] of this lane's j-th 8-k group
@@ -126,33 +154,38 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
       const half2_t p0 = sf_bitcast<half2_t>(xv.x), p1 = sf_bitcast<half2_t>(xv.y);
       const half2_t p2 = sf_bitcast<half2_t>(xv.z), p3 = sf_bitcast<half2_t>(xv.w);
       const half8_t a = half8_t{p0.x, p2.x, p0.y, p2.y, p1.x, p3.x, p1.y, p3.y};
-      // B: the same 8 weights, q - z exact in fp16
-      const uint32_t d = wv[i][j], d8 = d >> 8;
-      const half2_t v0 = sf_bitcast<half2_t>(and_or(d, 0x000F000Fu, 0x64006400u)) + c1;
-      const half2_t v1 = sf_bitcast<half2_t>(and_or(d, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
-      const half2_t v2 = sf_bitcast<half2_t>(and_or(d8, 0x000F000Fu, 0x64006400u)) + c1;
-      const half2_t v3 = sf_bitcast<half2_t>(and_or(d8, 0x00F000F0u, 0x64006400u)) * sixteenth + c2;
-      const half8_t bw = half8_t{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
-      part = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, j == 0 ? zero4 : part,
-                                                    0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        // B: the same 8 weights, q - z exact in fp16
+        const uint32_t d = wv[t][i][j], d8 = d >> 8;
+        const half2_t v0 = sf_bitcast<half2_t>(and_or(d, 0x000F000Fu, 0x64006400u)) + c1[t];
+        const half2_t v1 = sf_bitcast<half2_t>(and_or(d, 0x00F000F0u, 0x64006400u)) * sixteenth + c2[t];
+        const half2_t v2 = sf_bitcast<half2_t>(and_or(d8, 0x000F000Fu, 0x64006400u)) + c1[t];
+        const half2_t v3 = sf_bitcast<half2_t>(and_or(d8, 0x00F000F0u, 0x64006400u)) * sixteenth + c2[t];
+        const half8_t bw = half8_t{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, j == 0 ? zero4 : part[t], 0, 0, 0);
+      }
     }
-    {
-      uint32_t sb = sbits[i];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t sb = sbits[t][i];
       asm volatile("" : "+v"(sb));  // convert at the point of use (keeps the load in flight)
       const float s = (float)sf_bitcast<f16>((uint16_t)sb);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = i < cnt ? fmaf(part[r], s, acc[r]) : acc[r];
+      for (int r = 0; r < 4; ++r) acc[t][r] = i < cnt ? fmaf(part[t][r], s, acc[t][r]) : acc[t][r];
     }
   }
 
   // fold the waves (wave order) and store
   if (kg < 2) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][4 * kg + r][nl] = acc[r];
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][4 * kg + r][t * kTileN + nl] = acc[t][r];
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < B * kTileN; t += blockDim.x) {
-    const int b = t / kTileN, c = t - b * kTileN;
+  for (int e = threadIdx.x; e < B * T * kTileN; e += blockDim.x) {
+    const int b = e / (T * kTileN), c = e - b * (T * kTileN);
     const int row = n0 + c;
     if (row >= N) continue;
     float v = 0.f;
@@ -161,9 +194,10 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
   }
 }
 
-template <int LW, bool ASYM, int BPW>
+template <int LW, bool ASYM, int BPW, int T>
 void launch_one(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk) {
-  k_q4_gemv_mfma<LW, ASYM, BPW><<<grid, nw * 64, 0, a.s>>>(
+  static_assert(BPW > 0, "block count");
+  k_q4_gemv_mfma<LW, ASYM, BPW, T><<<grid, nw * 64, 0, a.s>>>(
       a.w, a.st, a.zt, (const f16 *)a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G,
       nblk);
 }
@@ -173,16 +207,21 @@ void launch_one(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk) {
 template <int LW> constexpr int kBucket[6] = {2, 4, 8, 12, 16, 24};
 template <> constexpr int kBucket<16>[6] = {1, 2, 4, 6, 8, 12};
 
-template <int LW, bool ASYM>
+template <int LW, bool ASYM, int T>
 void launch_bpw(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int bpw) {
   constexpr const int *bk = kBucket<LW>;
-#define SF_MB(I) launch_one<LW, ASYM, bk[I]>(a, grid, nw, nblk)
-  if (bpw == bk[0]) SF_MB(0);
-  else if (bpw == bk[1]) SF_MB(1);
-  else if (bpw == bk[2]) SF_MB(2);
-  else if (bpw == bk[3]) SF_MB(3);
-  else if (bpw == bk[4]) SF_MB(4);
-  else SF_MB(5);
+#define SF_MB(I) launch_one<LW, ASYM, bk[I], T>(a, grid, nw, nblk)
+  if constexpr (T > 1) {  // four tiles per wave: the two smallest block counts only
+    if (bpw == bk[0]) SF_MB(0);
+    else SF_MB(1);
+  } else {
+    if (bpw == bk[0]) SF_MB(0);
+    else if (bpw == bk[1]) SF_MB(1);
+    else if (bpw == bk[2]) SF_MB(2);
+    else if (bpw == bk[3]) SF_MB(3);
+    else if (bpw == bk[4]) SF_MB(4);
+    else SF_MB(5);
+  }
 #undef SF_MB
 }
 
@@ -195,8 +234,7 @@ namespace sf_gemv {
 bool mfma_gemv_applies(int B, int K, int g, int xdt) {
   const int lw = g % 128 == 0 ? 16 : 8;
   const int maxb = lw == 16 ? WLoad<16>::kMaxBpw : WLoad<8>::kMaxBpw;
-  return xdt == SF_F16 && B >= 3 && B <= 8 && (g == 64 || g == 128) &&
-         K / (8 * lw) <= kMaxWaves * maxb;
+  return xdt == SF_F16 && B >= 3 && B <= 8 && (g == 64 || g == 128) && K / (8 * lw) <= 8 * maxb;
 }
 
 // Waves per workgroup: enough that the grid holds about 3072 waves (three per
@@ -207,17 +245,41 @@ bool mfma_gemv_applies(int B, int K, int g, int xdt) {
 template <int LW>
 static void launch_lw(const GemvArgs &a) {
   const int nblk = a.K / (8 * LW);
-  const int grid = (a.N + kTileN - 1) / kTileN;
+  const int tiles = (a.N + kTileN - 1) / kTileN;
+  constexpr const int *bk = kBucket<LW>;
+  // Wide matrices (>= 512 row tiles) whose K fits two blocks per wave at 16
+  // waves: four row tiles per wave, so each activation fragment a wave loads
+  // feeds four MFMAs (the activation stream, which every workgroup reads
+  // whole from L2, shrinks four times).
+  {
+    const int grid = (tiles + 3) / 4;
+    int nw = 3072 / grid;
+    nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
+    const int need = (nblk + nw - 1) / nw;
+    if (tiles >= 512 && need <= bk[1]) {
+      const int bpw = need <= bk[0] ? bk[0] : bk[1];
+      nw = (nblk + bpw - 1) / bpw;
+      if (a.asym) launch_bpw<LW, true, 4>(a, grid, nw, nblk, bpw);
+      else launch_bpw<LW, false, 4>(a, grid, nw, nblk, bpw);
+      return;
+    }
+  }
+  const int grid = tiles;
   int nw = 3072 / grid;
   nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
-  int need = (nblk + nw - 1) / nw;
-  if (need > WLoad<LW>::kMaxBpw) need = (nblk + kMaxWaves - 1) / kMaxWaves;
-  int bpw = kBucket<LW>[5];
-  for (int b : kBucket<LW>)
-    if (b >= need) { bpw = b; break; }
+  auto pick = [&](int waves) {
+    int need = (nblk + waves - 1) / waves;
+    if (need > WLoad<LW>::kMaxBpw) need = (nblk + 7) / 8;
+    int b = bk[5];
+    for (int i = 0; i < 6; ++i)
+      if (bk[i] >= need) { b = bk[i]; break; }
+    return b;
+  };
+  int bpw = pick(nw);
+  if ((nblk + bpw - 1) / bpw > mfma_max_waves(LW, a.asym, bpw, 1)) bpw = pick(8);
   nw = (nblk + bpw - 1) / bpw;  // every launched wave has blocks
-  if (a.asym) launch_bpw<LW, true>(a, grid, nw, nblk, bpw);
-  else launch_bpw<LW, false>(a, grid, nw, nblk, bpw);
+  if (a.asym) launch_bpw<LW, true, 1>(a, grid, nw, nblk, bpw);
+  else launch_bpw<LW, false, 1>(a, grid, nw, nblk, bpw);
 }
 
 int launch_mfma_gemv(const GemvArgs &a, int g) {
