@@ -78,7 +78,9 @@ int sf_q4_unpack(const void *blob, int N, int K, int group_size, int has_zeros,
  * Q4Linear at T<=8 rows, q4_gemm_sym / q4_gemm_asym (bindings.cpp:98-150).
  * x: [B, K] of x_dtype (SF_F16 or SF_BF16). Outputs: y [B, N] of y_dtype
  * (SF_F16 / SF_BF16 / SF_F32), and/or y_f32 [B, N]; either may be NULL but
- * not both. bias: NULL or [N] of bias_dtype (added before the store). fp32
+ * not both. bias: NULL, [N] of bias_dtype (added before the store), or y_f32
+ * itself (fp32: each output adds its own previous value, per batch row — a
+ * residual add). fp32
  * accumulation throughout. */
 int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
                const void *bias, int bias_dtype, int B, int N, int K, int group_size,
@@ -100,6 +102,22 @@ int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtyp
 int sf_q4_gemv_fused(const void *blob, const float *src, int op, const float *norm_w, float eps,
                      int act_dtype, void *y, int y_dtype, float *y_f32, const void *bias,
                      int bias_dtype, int N, int K, int group_size, int has_zeros, void *stream);
+
+/* sf_q4_gemv_fused over B = 1..8 rows (src [B][K], or [B][2K] gate|up): the
+ * target's verify rows of speculative decoding (engine/speculative.py:280)
+ * with each RMSNorm / SwiGLU folded into the next projection as the decode
+ * step does. B = 1 is sf_q4_gemv_fused; B = 3..8 with fp16 activations runs
+ * the batch MFMA GEMV with the producer folded into its activation load, and
+ * equals sf_rmsnorm / sf_silu_mul followed by sf_q4_gemv bit for bit. Other
+ * shapes return SF_EUNSUPPORTED; sf_q4_gemv_fused_rows_supported says which
+ * (1 = supported). bias may be y_f32 itself (each row adds its own previous
+ * value), as for sf_q4_gemv. */
+int sf_q4_gemv_fused_rows_supported(int op, int B, int N, int K, int group_size, int has_zeros,
+                                    int act_dtype);
+int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op, const float *norm_w,
+                          float eps, int act_dtype, void *y, int y_dtype, float *y_f32,
+                          const void *bias, int bias_dtype, int B, int N, int K, int group_size,
+                          int has_zeros, void *stream);
 
 /* ---- prefill GEMM (M rows) ------------------------------------------------
  * Y[m, n] = X[m, :] . dequant(W)[n, :] for M rows; replaces q4_gemm_sym /
@@ -236,9 +254,11 @@ int sf_lm_head_argmax_rmsnorm(const void *w, const float *h, const float *norm_w
  * verify of K+1 = B positions in greedy speculative decoding
  * (/root/reference/siliconfer/engine/speculative.py:166-189, which takes the
  * argmax of each verify row of `t_log`). x [B, H] (x_dtype); logits [B, V]
- * fp32 or NULL; tokens_out[b] = argmax of row b (lowest index on ties). Each
- * row's logits equal sf_lm_head_argmax's for that row alone, bit for bit.
- * Needs B * H * sizeof(x element) <= 65536. The workspace
+ * fp32 or NULL; tokens_out[b] = argmax of row b (lowest index on ties).
+ * From 3 rows, fp16 / bf16 rows with H % 32 == 0 and H <= 2048 run on MFMA
+ * (exact products, fp32 sums); the others on the VALU, where each row's logits equal
+ * sf_lm_head_argmax's for that row alone, bit for bit. Needs
+ * B * H * sizeof(x element) <= 65536. The workspace
  * (sf_lm_head_rows_workspace_bytes, 256-byte aligned) is zero-filled before
  * its first use; each call leaves it so. */
 size_t sf_lm_head_rows_workspace_bytes(int V, int B);

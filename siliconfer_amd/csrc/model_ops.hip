@@ -468,6 +468,170 @@ k_lm_head_rows(const uint16_t *__restrict__ w, const void *__restrict__ x,
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// The same B <= 8 rows on MFMA (fp16 / bf16 activations, H % 32 == 0,
+// H <= 2048): v_mfma_f32_16x16x32_bf16 with the batch as the A operand, each
+// activation split exactly into a bf16 high part (A rows 0..7) and the
+// remainder (rows 8..15; an fp16 value has 11 significant bits, so the
+// remainder has at most 3 and is exact in bf16, a bf16 one has none), and 16
+// table rows as the B operand. Products are exact (bf16 x bf16) and summed in
+// fp32; logit = C[b] + C[8 + b]. The VALU kernel above spends 8 fma per table
+// element at B = 8; here the MFMA does that work and the kernel streams the
+// table. The activations sit in LDS in fragment order: fragment
+// (ks * 4 + kg) * 16 + i is the 8 bf16 of A row i at k = 32 ks + 8 kg .. +7,
+// so lane l reads fragment (ks * 4 + l / 16) * 16 + l % 16: one linear 16-byte
+// read per lane, no bank conflict.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+template <int XDT>
+__global__ void __launch_bounds__(kThreads)
+k_lm_head_rows_mfma(const uint16_t *__restrict__ w, const void *__restrict__ x,
+                    float *__restrict__ logits, int V, int H, int B,
+                    int32_t *__restrict__ tokens_out, float *part_val, int *part_idx,
+                    unsigned *counter) {
+  extern __shared__ __attribute__((aligned(16))) u32x4 xa[];  // [H / 32 * 4][16] fragments
+  __shared__ float bv_s[kRowsMax][kThreads / 64];
+  __shared__ int bi_s[kRowsMax][kThreads / 64];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nks = H >> 5;
+  for (int f = tid; f < nks * 64; f += kThreads) {
+    const int i = f & 15, kgs = f >> 4;
+    const int b = i & 7;
+    uint32_t pk[4];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      uint32_t h2[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int k = kgs * 8 + e2 * 2 + t;
+        const float v = b < B ? sf_load_as_f32<XDT>(x, (size_t)b * H + k) : 0.f;
+        const uint32_t hi = sf_bitcast<uint32_t>(v) & 0xffff0000u;
+        h2[t] = i < 8 ? hi >> 16 : sf_bitcast<uint32_t>(v - sf_bitcast<float>(hi)) >> 16;
+      }
+      pk[e2] = h2[0] | h2[1] << 16;
+    }
+    xa[f] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+  }
+  __syncthreads();
+
+  const int nt = (V + 15) >> 4;
+  const int n_waves = gridDim.x * (kThreads / 64);
+  const int gw = blockIdx.x * (kThreads / 64) + wave;
+  const int i16 = lane & 15, kg = lane >> 4;
+  // lane l < 32 tracks batch rows 4 (l / 16) + r, r = 0..3
+  float best[4];
+  int best_i[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    best[r] = -INFINITY;
+    best_i[r] = 0x7fffffff;
+  }
+  constexpr int KQ = 8;  // table loads in flight per lane
+  for (int t = gw; t < nt; t += n_waves) {
+    const int v0 = t * 16;
+    const uint16_t *wr = w + (size_t)min(v0 + i16, V - 1) * H + kg * 8;
+    float4_t c = {0.f, 0.f, 0.f, 0.f};
+    for (int ks0 = 0; ks0 < nks; ks0 += KQ) {
+      u32x4 wv[KQ];
+#pragma unroll
+      for (int q = 0; q < KQ; ++q)
+        wv[q] = __builtin_nontemporal_load((const u32x4 *)(wr + (size_t)min(ks0 + q, nks - 1) * 32));
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        if (ks0 + q >= nks) break;  // uniform
+        const u32x4 a = xa[((ks0 + q) * 4 + kg) * 16 + i16];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sf_bitcast<bf16x8_t>(a),
+                                                    sf_bitcast<bf16x8_t>(wv[q]), c, 0, 0, 0);
+      }
+    }
+    // lane l holds C[4 (l / 16) + r][l % 16]: rows 0..7 are the high parts,
+    // 8..15 the remainders of the same batch rows, 32 lanes apart
+    const int vv = v0 + i16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float sum = c[r] + __shfl_xor(c[r], 32, 64);
+      const int b = 4 * (kg & 1) + r;
+      if (kg < 2 && b < B && vv < V) {
+        if (logits) logits[(size_t)b * V + vv] = sum;
+        if (better(sum, vv, best[r], best_i[r])) {
+          best[r] = sum;
+          best_i[r] = vv;
+        }
+      }
+    }
+  }
+  // fold each batch row over its 16 lanes, then the waves through LDS
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const float ov = __shfl_xor(best[r], off, 64);
+      const int oi = __shfl_xor(best_i[r], off, 64);
+      if (better(ov, oi, best[r], best_i[r])) {
+        best[r] = ov;
+        best_i[r] = oi;
+      }
+    }
+  }
+  if (lane == 0 || lane == 16) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bv_s[4 * (lane >> 4) + r][wave] = best[r];
+      bi_s[4 * (lane >> 4) + r][wave] = best_i[r];
+    }
+  }
+  __syncthreads();
+  if (tid < B) {
+    float bb = bv_s[tid][0];
+    int bi = bi_s[tid][0];
+    for (int k = 1; k < kThreads / 64; ++k)
+      if (better(bv_s[tid][k], bi_s[tid][k], bb, bi)) {
+        bb = bv_s[tid][k];
+        bi = bi_s[tid][k];
+      }
+    __hip_atomic_store((uint32_t *)(part_val + (size_t)tid * gridDim.x + blockIdx.x),
+                       sf_bitcast<uint32_t>(bb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(part_idx + (size_t)tid * gridDim.x + blockIdx.x, bi, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (int b = wave; b < B; b += kThreads / 64) {
+    float bb = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int k = lane; k < (int)gridDim.x; k += 64) {
+      const float v = sf_bitcast<float>(__hip_atomic_load(
+          (const uint32_t *)(part_val + (size_t)b * gridDim.x + k), __ATOMIC_RELAXED,
+          __HIP_MEMORY_SCOPE_AGENT));
+      const int i = __hip_atomic_load(part_idx + (size_t)b * gridDim.x + k, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      if (better(v, i, bb, bi)) {
+        bb = v;
+        bi = i;
+      }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bb, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (better(ov, oi, bb, bi)) {
+        bb = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) tokens_out[b] = bi == 0x7fffffff ? 0 : bi;
+  }
+  __syncthreads();
+  if (tid == 0)  // ready for the next call on this workspace
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -632,6 +796,19 @@ extern "C" int sf_lm_head_argmax_rows(const void *w, const void *x, int x_dtype,
   int *pi = (int *)(pv + (size_t)B * kHeadBlocks);
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *wb = (const uint16_t *)w;
+  // MFMA from 3 rows (measured at V = 151936, H = 896: 86 / 99 us at 4 / 8
+  // rows against 96 / 162 on the VALU; at 1-2 rows the VALU's contiguous
+  // table reads win, 56 / 66 against 80 / 85)
+  if (B >= 3 && x_dtype != SF_F32 && H % 32 == 0 && (size_t)H * 32 <= kRowsLdsBytes) {
+    const size_t lds_a = (size_t)H * 32;  // 16 A rows of bf16 fragments
+    if (x_dtype == SF_F16)
+      k_lm_head_rows_mfma<SF_F16><<<kHeadBlocks, kThreads, lds_a, st>>>(wb, x, logits, V, H, B,
+                                                                        tokens_out, pv, pi, counter);
+    else
+      k_lm_head_rows_mfma<SF_BF16><<<kHeadBlocks, kThreads, lds_a, st>>>(wb, x, logits, V, H, B,
+                                                                         tokens_out, pv, pi, counter);
+    return sf_check_launch("sf_lm_head_argmax_rows");
+  }
   if (x_dtype == SF_F32)
     k_lm_head_rows<SF_F32><<<kHeadBlocks, kThreads, lds, st>>>(wb, x, logits, V, H, B, tokens_out,
                                                                pv, pi, counter);

@@ -3,7 +3,8 @@
 
 namespace sf_gemv {
 bool mfma_gemv_applies(int B, int K, int g, int xdt);
-int launch_mfma_gemv(const GemvArgs &a, int g);
+bool mfma_gemv_pre_applies(int B, int N, int K, int g, bool asym, int pre);
+int launch_mfma_gemv(const GemvArgs &a, int g, int pre, const float *pre_w, float eps);
 extern template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_BF16>(const GemvPlan &, const GemvArgs &);
 extern template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
@@ -13,6 +14,14 @@ extern template void launch_pre<SF_F32>(const GemvPlan &, const GemvArgs &, int,
 }  // namespace sf_gemv
 
 using namespace sf_gemv;
+
+static bool mfma_gemv_enabled() {
+  static const bool ok = [] {
+    const char *e = getenv("SF_GEMV_MFMA");
+    return !(e && e[0] == '0');
+  }();
+  return ok;
+}
 
 extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
                           float *y_f32, const void *bias, int bias_dtype, int B, int N, int K,
@@ -44,12 +53,8 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
                 (hipStream_t)stream};
   // batch 3..8, fp16 activations, groups of 64 or 128: the MFMA kernel
   // (SF_GEMV_MFMA=0 keeps the VALU one)
-  static const bool mfma_ok = [] {
-    const char *e = getenv("SF_GEMV_MFMA");
-    return !(e && e[0] == '0');
-  }();
-  if (mfma_ok && mfma_gemv_applies(B, K, group_size, x_dtype)) {
-    launch_mfma_gemv(args, group_size);
+  if (mfma_gemv_enabled() && mfma_gemv_applies(B, K, group_size, x_dtype)) {
+    launch_mfma_gemv(args, group_size, PRE_NONE, nullptr, 0.f);
   } else if (x_dtype == SF_F16) {
     launch_x<SF_F16>(pl, args);
   } else if (x_dtype == SF_BF16) {
@@ -63,6 +68,7 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
       sl.x = (const float *)x + (size_t)b0 * K;
       if (y) sl.y = (char *)y + (size_t)b0 * N * ysz;
       if (y_f32) sl.y32 = y_f32 + (size_t)b0 * N;
+      if (bias && bias == (const void *)y_f32) sl.bias = sl.y32;  // per-row residual
       GemvPlan p2;
       plan_gemv(sl.B, N, K, group_size, x_dtype, &p2);
       launch_x<SF_F32>(p2, sl);
@@ -107,4 +113,54 @@ extern "C" int sf_q4_gemv_fused(const void *blob, const float *src, int op, cons
   else if (act_dtype == SF_BF16) launch_pre<SF_BF16>(pl, args, pre, norm_w, eps);
   else launch_pre<SF_F32>(pl, args, pre, norm_w, eps);
   return sf_check_launch("sf_q4_gemv_fused");
+}
+
+extern "C" int sf_q4_gemv_fused_rows_supported(int op, int B, int N, int K, int group_size,
+                                               int has_zeros, int act_dtype) {
+  if ((op != SF_PRE_RMSNORM && op != SF_PRE_SILU_MUL) || N <= 0 || K <= 0 || group_size <= 0 ||
+      K % group_size || group_size % 32)
+    return 0;
+  if (B == 1) return 1;
+  return mfma_gemv_enabled() && act_dtype == SF_F16 &&
+         mfma_gemv_pre_applies(B, N, K, group_size, has_zeros != 0,
+                               op == SF_PRE_RMSNORM ? PRE_RMSNORM : PRE_SILU);
+}
+
+extern "C" int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op,
+                                     const float *norm_w, float eps, int act_dtype, void *y,
+                                     int y_dtype, float *y_f32, const void *bias, int bias_dtype,
+                                     int B, int N, int K, int group_size, int has_zeros,
+                                     void *stream) {
+  SF_REQUIRE(B >= 1 && B <= 8, SF_EINVAL, "GEMV batch must be 1..8 (got %d)", B);
+  if (B == 1)
+    return sf_q4_gemv_fused(blob, src, op, norm_w, eps, act_dtype, y, y_dtype, y_f32, bias,
+                            bias_dtype, N, K, group_size, has_zeros, stream);
+  SF_REQUIRE(N > 0 && K > 0 && group_size > 0, SF_EINVAL, "invalid shape N=%d K=%d group_size=%d",
+             N, K, group_size);
+  SF_REQUIRE(K % group_size == 0, SF_EINVAL, "in_features must be divisible by group_size");
+  SF_REQUIRE(op == SF_PRE_RMSNORM || op == SF_PRE_SILU_MUL, SF_EINVAL, "bad fused op %d", op);
+  SF_REQUIRE(blob && src && (y || y_f32) && (op != SF_PRE_RMSNORM || norm_w), SF_EINVAL,
+             "null pointer argument");
+  SF_REQUIRE(y_dtype == SF_F16 || y_dtype == SF_BF16 || y_dtype == SF_F32, SF_EINVAL,
+             "bad output dtype %d", y_dtype);
+  SF_REQUIRE(!bias || bias_dtype == SF_F16 || bias_dtype == SF_BF16 || bias_dtype == SF_F32,
+             SF_EINVAL, "bad bias dtype %d", bias_dtype);
+  SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)src & 15) == 0 &&
+                 ((uintptr_t)norm_w & 15) == 0,
+             SF_EINVAL, "blob must be 256-byte aligned, src and norm_w 16-byte aligned");
+  SF_REQUIRE(sf_q4_gemv_fused_rows_supported(op, B, N, K, group_size, has_zeros, act_dtype),
+             SF_EUNSUPPORTED,
+             "fused op %d at batch %d (N=%d K=%d group_size=%d act dtype %d): this build folds "
+             "the producer at batch 1, and at 3..8 for fp16 activations on plans of at most four "
+             "MFMAs per lane; run sf_rmsnorm / sf_silu_mul and sf_q4_gemv instead",
+             op, B, N, K, group_size, act_dtype);
+  BlobLayout L;
+  sf_blob_layout(N, K, group_size, has_zeros, &L);
+  const uint8_t *w = (const uint8_t *)blob;
+  const f16 *st = (const f16 *)(w + L.s_off);
+  const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
+  GemvArgs args{w, st, zt, src, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, L.G, has_zeros != 0,
+                (hipStream_t)stream};
+  launch_mfma_gemv(args, group_size, op == SF_PRE_RMSNORM ? PRE_RMSNORM : PRE_SILU, norm_w, eps);
+  return sf_check_launch("sf_q4_gemv_fused_rows");
 }

@@ -144,10 +144,13 @@ __device__ __forceinline__ void butterfly(float (&v)[B][R], int p) {
 template <int V>
 constexpr int clog2() { return V <= 1 ? 0 : 1 + clog2<V / 2>(); }
 
+// bias: [N] added to every batch row, or y32 itself (fp32): each output then
+// adds its own previous value (a residual add, per batch row)
 __device__ __forceinline__ void store_out(void *y, int ydt, float *y32, const void *bias, int bdt,
                                           size_t idx, int row, float v) {
   if (bias) {
-    if (bdt == SF_F32) v += ((const float *)bias)[row];
+    if (bias == y32) v += y32[idx];
+    else if (bdt == SF_F32) v += ((const float *)bias)[row];
     else if (bdt == SF_F16) v += (float)((const f16 *)bias)[row];
     else v += sf_bf16_to_f32(((const uint16_t *)bias)[row]);
   }

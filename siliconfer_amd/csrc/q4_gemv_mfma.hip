@@ -52,28 +52,46 @@ template <> struct WLoad<8> { typedef u32x2 T; static constexpr int kMaxBpw = 24
 template <> struct WLoad<16> { typedef u32x4 T; static constexpr int kMaxBpw = 12; };
 
 // Waves per workgroup a variant may use: 16 where its registers fit the
-// 128-VGPR budget of a 1024-thread workgroup, else 8 (256 VGPRs).
-__host__ __device__ constexpr int mfma_max_waves(int LW, bool asym, int bpw, int T) {
-  return (T > 1 || bpw * LW <= (asym ? 64 : 128)) ? 16 : 8;
+// 128-VGPR budget of a 1024-thread workgroup, else 8 (256 VGPRs); always 8
+// for the folded RMSNorm, which holds a row norm's loads as well, and 16 for
+// the folded SwiGLU only at the smaller block counts (its source ring).
+__host__ __device__ constexpr int mfma_max_waves(int LW, bool asym, int bpw, int T, int pre = 0) {
+  return pre == 1   ? 8
+         : pre == 2 ? ((T > 1 ? bpw <= 2 : bpw * LW <= (asym ? 64 : 96)) ? 16 : 8)
+                    : ((T > 1 || bpw * LW <= (asym ? 64 : 128)) ? 16 : 8);
 }
 
-template <int LW, bool ASYM, int BPW, int T>
-__global__ void __launch_bounds__(mfma_max_waves(LW, ASYM, BPW, T) * 64)
+// PRE folds the producer of the activations into their load, as the batch-1
+// VALU GEMV does (x is then the fp32 source): PRE_RMSNORM x[b] = src[b] *
+// inv_rms(src[b]) * pre_w with the norm of sf_row_inv_rms (the waves of a
+// workgroup take the batch rows in turn and pass the norms through LDS),
+// PRE_SILU x[b][k] = silu(src[b][k]) * src[b][K + k]; each value is rounded
+// to fp16 as sf_rmsnorm / sf_silu_mul store it, so the result equals those
+// kernels followed by this GEMV with the same plan. A lane loads the fp32
+// sources of all its blocks ahead of the weights (so waiting for them never
+// waits for the weight stream), which is why the host folds only plans of at
+// most four MFMAs per lane; each block becomes fp16 operands just before its
+// MFMAs.
+template <int LW, bool ASYM, int BPW, int T, int PRE>
+__global__ void __launch_bounds__(mfma_max_waves(LW, ASYM, BPW, T, PRE) * 64)
 k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
-               const uint8_t *__restrict__ ztile, const f16 *__restrict__ x, void *__restrict__ y,
+               const uint8_t *__restrict__ ztile, const void *__restrict__ x, void *__restrict__ y,
                int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt, int B,
-               int N, int K, int G, int nblk) {
+               int N, int K, int G, int nblk, const float *__restrict__ pre_w, float eps) {
   constexpr int KB = 8 * LW;   // k per block
   constexpr int NM = LW / 4;   // MFMAs per block (one per weight dword)
   // activation ring: every block when they fit in 64 registers, else XR blocks
-  // loaded XR - 1 ahead
+  // loaded XR - 1 ahead (folded producers: every block's sources)
   constexpr int XR = BPW * NM <= 16 ? BPW : 16 / NM;
   constexpr int XPRE = XR == BPW ? BPW : XR - 1;
+  static_assert(PRE == sf_gemv::PRE_NONE || BPW * NM <= 4, "folded producers: four MFMAs per lane");
   typedef typename WLoad<LW>::T wvec_t;
   __shared__ float red[kMaxWaves][8][T * kTileN];
 
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv_row0 = wave;  // RMSNorm: batch rows wave, wave + nw, ...
+  __shared__ float inv_s[8];
   const int nl = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * T * kTileN;
   int nt[T];
@@ -89,10 +107,39 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
   const int xoff = nl < B ? (nl * K + kg * 2 * LW) * 2 : 0x40000000;
   u32x4 xs[XR][NM];
   auto xload = [&](int i) {
-    const int o = xoff + min(blk0 + i, blast) * KB * 2;
+    if constexpr (PRE == sf_gemv::PRE_NONE) {
+      const int o = xoff + min(blk0 + i, blast) * KB * 2;
 #pragma unroll
-    for (int j = 0; j < NM; ++j) xs[i % XR][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, o + j * 16, 0, 0);
+      for (int j = 0; j < NM; ++j) xs[i % XR][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, o + j * 16, 0, 0);
+    }
   };
+  // folded producer: the lane's fp32 source (and norm weights / up half) of
+  // every block, then (RMSNorm) the norm of the wave's first batch row
+  float4_t fa[BPW][NM][2], fb[BPW][NM][2];
+  SfRowNorm nrm;
+  const float *srow = (const float *)x +
+      (size_t)min(nl, B - 1) * (PRE == sf_gemv::PRE_SILU ? 2 * (size_t)K : (size_t)K);
+  auto pload = [&](int i) {
+    if constexpr (PRE != sf_gemv::PRE_NONE) {
+#pragma unroll
+      for (int j = 0; j < NM; ++j) {
+        const int k = min(blk0 + i, blast) * KB + kg * 2 * LW + 8 * j;
+        const float4_t *pa = (const float4_t *)(srow + k);
+        const float4_t *pb = PRE == sf_gemv::PRE_SILU ? (const float4_t *)(srow + K + k)
+                                                      : (const float4_t *)(pre_w + k);
+        fa[i][j][0] = pa[0];
+        fa[i][j][1] = pa[1];
+        fb[i][j][0] = pb[0];
+        fb[i][j][1] = pb[1];
+      }
+    }
+  };
+  if constexpr (PRE != sf_gemv::PRE_NONE) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) pload(i);
+    if constexpr (PRE == sf_gemv::PRE_RMSNORM)
+      if (wv_row0 < B) nrm.issue<true>((const float *)x + (size_t)wv_row0 * K, nullptr, K);
+  }
 #pragma unroll
   for (int i = 0; i < XPRE; ++i) xload(i);
 
@@ -119,6 +166,37 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
   // interleave them with the MFMAs to save registers)
   __builtin_amdgcn_sched_barrier(0);
 
+  float inv = 1.f;
+  if constexpr (PRE == sf_gemv::PRE_RMSNORM) {
+    const float *src = (const float *)x;
+    for (int b = wv_row0; b < B; b += nw) {  // uniform per wave; all lanes active
+      if (b != wv_row0) nrm.issue<true>(src + (size_t)b * K, nullptr, K);
+      const float r = nrm.finish(src + (size_t)b * K, nullptr, K, eps);
+      if (lane == 0) inv_s[b] = r;
+    }
+    __syncthreads();
+    inv = inv_s[min(nl, B - 1)];
+  }
+  // block i's sources -> its fp16 operands (folded producers)
+  auto pconvert = [&](int i) {
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int q = 2 * e + t;
+          const float a = fa[i][j][q >> 2][q & 3], g = fb[i][j][q >> 2][q & 3];
+          v2[t] = PRE == sf_gemv::PRE_RMSNORM ? sf_opaque(a * inv * g) : sf_silu_mul(a, g);
+        }
+        pk[e] = sf_bitcast<uint32_t>(half2_t{(f16)v2[0], (f16)v2[1]});
+      }
+      xs[i % XR][j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+  };
+
   const half2_t sixteenth = {(f16)0.0625f, (f16)0.0625f};
   const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   float4_t part[T];
@@ -132,6 +210,7 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     if (i + XPRE < BPW) xload(i + XPRE);
+    if constexpr (PRE != sf_gemv::PRE_NONE) pconvert(i);
     // blocks i >= cnt (only in a workgroup's last wave) are computed on re-read
     // data and dropped at the scale step by a select: a branch here would let
     // the compiler sink this block's loads into it, after the wait
@@ -195,11 +274,26 @@ k_q4_gemv_mfma(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
 }
 
 template <int LW, bool ASYM, int BPW, int T>
-void launch_one(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk) {
-  static_assert(BPW > 0, "block count");
-  k_q4_gemv_mfma<LW, ASYM, BPW, T><<<grid, nw * 64, 0, a.s>>>(
-      a.w, a.st, a.zt, (const f16 *)a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G,
-      nblk);
+void launch_one(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int pre,
+                const float *pre_w, float eps) {
+  using namespace sf_gemv;
+  if constexpr (BPW * (LW / 4) <= 4) {
+    if (pre == PRE_RMSNORM) {
+      k_q4_gemv_mfma<LW, ASYM, BPW, T, PRE_RMSNORM><<<grid, nw * 64, 0, a.s>>>(
+          a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G, nblk, pre_w,
+          eps);
+      return;
+    }
+    if (pre == PRE_SILU) {
+      k_q4_gemv_mfma<LW, ASYM, BPW, T, PRE_SILU><<<grid, nw * 64, 0, a.s>>>(
+          a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G, nblk, pre_w,
+          eps);
+      return;
+    }
+  }
+  k_q4_gemv_mfma<LW, ASYM, BPW, T, PRE_NONE><<<grid, nw * 64, 0, a.s>>>(
+      a.w, a.st, a.zt, a.x, a.y, a.ydt, a.y32, a.bias, a.bdt, a.B, a.N, a.K, a.G, nblk, nullptr,
+      0.f);
 }
 
 // Compiled blocks-per-wave counts: 8-byte lanes {2, 4, 8, 12, 16, 24},
@@ -208,9 +302,10 @@ template <int LW> constexpr int kBucket[6] = {2, 4, 8, 12, 16, 24};
 template <> constexpr int kBucket<16>[6] = {1, 2, 4, 6, 8, 12};
 
 template <int LW, bool ASYM, int T>
-void launch_bpw(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int bpw) {
+void launch_bpw(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int bpw, int pre,
+                const float *pre_w, float eps) {
   constexpr const int *bk = kBucket<LW>;
-#define SF_MB(I) launch_one<LW, ASYM, bk[I], T>(a, grid, nw, nblk)
+#define SF_MB(I) launch_one<LW, ASYM, bk[I], T>(a, grid, nw, nblk, pre, pre_w, eps)
   if constexpr (T > 1) {  // four tiles per wave: the two smallest block counts only
     if (bpw == bk[0]) SF_MB(0);
     else SF_MB(1);
@@ -227,6 +322,66 @@ void launch_bpw(const sf_gemv::GemvArgs &a, int grid, int nw, int nblk, int bpw)
 
 }  // namespace
 
+// Waves per workgroup: enough that the grid holds about 3072 waves (three per
+// SIMD: all of the matrix in flight at once), at most 16, and at least enough
+// that no wave takes more than the largest block count. Blocks per wave: the
+// smallest compiled count that covers the share, so only the last wave has a
+// remainder. Wide matrices (>= 512 row tiles) whose K fits two blocks per
+// wave at 16 waves run four row tiles per wave, so each activation fragment a
+// wave loads feeds four MFMAs (the activation stream, which every workgroup
+// reads whole from L2, shrinks four times).
+struct MfmaPlan { int LW, T, grid, nw, nblk, bpw; };
+
+static MfmaPlan mfma_plan(int N, int K, int g, bool asym) {
+  MfmaPlan p;
+  p.LW = g % 128 == 0 ? 16 : 8;
+  p.nblk = K / (8 * p.LW);
+  const int tiles = (N + kTileN - 1) / kTileN;
+  const int *bk = p.LW == 16 ? kBucket<16> : kBucket<8>;
+  const int maxb = p.LW == 16 ? WLoad<16>::kMaxBpw : WLoad<8>::kMaxBpw;
+  {
+    const int grid = (tiles + 3) / 4;
+    int nw = 3072 / grid;
+    nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
+    const int need = (p.nblk + nw - 1) / nw;
+    if (tiles >= 512 && need <= bk[1]) {
+      p.T = 4;
+      p.grid = grid;
+      p.bpw = need <= bk[0] ? bk[0] : bk[1];
+      p.nw = (p.nblk + p.bpw - 1) / p.bpw;
+      return p;
+    }
+  }
+  p.T = 1;
+  p.grid = tiles;
+  int nw = 3072 / p.grid;
+  nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
+  auto pick = [&](int waves) {
+    int need = (p.nblk + waves - 1) / waves;
+    if (need > maxb) need = (p.nblk + 7) / 8;
+    int b = bk[5];
+    for (int i = 0; i < 6; ++i)
+      if (bk[i] >= need) { b = bk[i]; break; }
+    return b;
+  };
+  p.bpw = pick(nw);
+  if ((p.nblk + p.bpw - 1) / p.bpw > mfma_max_waves(p.LW, asym, p.bpw, 1)) p.bpw = pick(8);
+  p.nw = (p.nblk + p.bpw - 1) / p.bpw;  // every launched wave has blocks
+  return p;
+}
+
+template <int LW>
+static void launch_plan(const sf_gemv::GemvArgs &a, const MfmaPlan &p, int pre,
+                        const float *pre_w, float eps) {
+  if (p.T == 4) {
+    if (a.asym) launch_bpw<LW, true, 4>(a, p.grid, p.nw, p.nblk, p.bpw, pre, pre_w, eps);
+    else launch_bpw<LW, false, 4>(a, p.grid, p.nw, p.nblk, p.bpw, pre, pre_w, eps);
+  } else {
+    if (a.asym) launch_bpw<LW, true, 1>(a, p.grid, p.nw, p.nblk, p.bpw, pre, pre_w, eps);
+    else launch_bpw<LW, false, 1>(a, p.grid, p.nw, p.nblk, p.bpw, pre, pre_w, eps);
+  }
+}
+
 namespace sf_gemv {
 
 // Batch 3..8, fp16 activations, group size 64 or 128 (one 8- or 16-byte-lane
@@ -237,54 +392,19 @@ bool mfma_gemv_applies(int B, int K, int g, int xdt) {
   return xdt == SF_F16 && B >= 3 && B <= 8 && (g == 64 || g == 128) && K / (8 * lw) <= 8 * maxb;
 }
 
-// Waves per workgroup: enough that the grid holds about 3072 waves (three per
-// SIMD: all of the matrix in flight at once), at most 8, and at least enough
-// that no wave takes more than the largest block count. Blocks per wave: the
-// smallest compiled count that covers the share, so only the last wave has a
-// remainder.
-template <int LW>
-static void launch_lw(const GemvArgs &a) {
-  const int nblk = a.K / (8 * LW);
-  const int tiles = (a.N + kTileN - 1) / kTileN;
-  constexpr const int *bk = kBucket<LW>;
-  // Wide matrices (>= 512 row tiles) whose K fits two blocks per wave at 16
-  // waves: four row tiles per wave, so each activation fragment a wave loads
-  // feeds four MFMAs (the activation stream, which every workgroup reads
-  // whole from L2, shrinks four times).
-  {
-    const int grid = (tiles + 3) / 4;
-    int nw = 3072 / grid;
-    nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
-    const int need = (nblk + nw - 1) / nw;
-    if (tiles >= 512 && need <= bk[1]) {
-      const int bpw = need <= bk[0] ? bk[0] : bk[1];
-      nw = (nblk + bpw - 1) / bpw;
-      if (a.asym) launch_bpw<LW, true, 4>(a, grid, nw, nblk, bpw);
-      else launch_bpw<LW, false, 4>(a, grid, nw, nblk, bpw);
-      return;
-    }
-  }
-  const int grid = tiles;
-  int nw = 3072 / grid;
-  nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
-  auto pick = [&](int waves) {
-    int need = (nblk + waves - 1) / waves;
-    if (need > WLoad<LW>::kMaxBpw) need = (nblk + 7) / 8;
-    int b = bk[5];
-    for (int i = 0; i < 6; ++i)
-      if (bk[i] >= need) { b = bk[i]; break; }
-    return b;
-  };
-  int bpw = pick(nw);
-  if ((nblk + bpw - 1) / bpw > mfma_max_waves(LW, a.asym, bpw, 1)) bpw = pick(8);
-  nw = (nblk + bpw - 1) / bpw;  // every launched wave has blocks
-  if (a.asym) launch_bpw<LW, true, 1>(a, grid, nw, nblk, bpw);
-  else launch_bpw<LW, false, 1>(a, grid, nw, nblk, bpw);
+// The folded producers run the plan of the plain GEMV (so the results agree
+// bit for bit) when its waves hold at most four MFMAs' sources and fit the
+// folded kernels' wave limit.
+bool mfma_gemv_pre_applies(int B, int N, int K, int g, bool asym, int pre) {
+  if (!mfma_gemv_applies(B, K, g, SF_F16)) return false;
+  const MfmaPlan p = mfma_plan(N, K, g, asym);
+  return p.bpw * (p.LW / 4) <= 4 && p.nw <= mfma_max_waves(p.LW, asym, p.bpw, p.T, pre);
 }
 
-int launch_mfma_gemv(const GemvArgs &a, int g) {
-  if (g % 128 == 0) launch_lw<16>(a);
-  else launch_lw<8>(a);
+int launch_mfma_gemv(const GemvArgs &a, int g, int pre, const float *pre_w, float eps) {
+  const MfmaPlan p = mfma_plan(a.N, a.K, g, a.asym);
+  if (p.LW == 16) launch_plan<16>(a, p, pre, pre_w, eps);
+  else launch_plan<8>(a, p, pre, pre_w, eps);
   return SF_OK;
 }
 

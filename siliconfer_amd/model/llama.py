@@ -153,6 +153,7 @@ class LlamaModel:
         self.pos = 0
         self.graph = None
         self._verify_graphs = {}
+        self._rows_plans = {}
         self._vbufs = None
         self._prefill_bufs = None
         self._gemm_ws = None
@@ -436,18 +437,53 @@ class LlamaModel:
             self.vtok.data_ptr(), self.rows_ws.data_ptr(), self.rows_ws.numel(), self._st()),
             "sf_lm_head_argmax_rows")
 
+    def _rows_plan(self, T: int) -> tuple[bool, bool, bool, bool]:
+        """How T rows run: (residual, fold_qkv, fold_gate_up, fold_down).
+        residual: up to 8 rows every projection is a batch GEMV and the o /
+        down projections add into the residual rows themselves (the norms then
+        read them directly). fold_*: the RMSNorm / SwiGLU before that
+        projection runs inside it (batch 1, or 3..8 rows at fp16 on the batch
+        MFMA GEMV where its plan allows) — each choice gives the same bits."""
+        if T not in self._rows_plans:
+            L0 = self.layers[0]
+            residual = T <= 8 and L0.o.in_features <= 16384 and L0.down.in_features <= 16384
+            ok = lambda op, w: bool(self.fuse and residual and self.lib.sf_q4_gemv_fused_rows_supported(
+                op, T, w.out_features, w.in_features, w.group_size, int(w.has_zeros),
+                _DT[self.act_dtype]))
+            self._rows_plans[T] = (residual, ok(_lib.SF_PRE_RMSNORM, L0.qkv),
+                                   ok(_lib.SF_PRE_RMSNORM, L0.gate_up),
+                                   ok(_lib.SF_PRE_SILU_MUL, L0.down))
+        return self._rows_plans[T]
+
+    def _gemv_fused_rows(self, w: Q4Weight, src, op: int, norm_w, y32, bias, T: int):
+        self._chk(self.lib.sf_q4_gemv_fused_rows(
+            w.blob.data_ptr(), src.data_ptr(), op, None if norm_w is None else norm_w.data_ptr(),
+            float(self.config.rms_norm_eps), _DT[self.act_dtype], None, _lib.SF_F32, y32.data_ptr(),
+            None if bias is None else bias.data_ptr(), _lib.SF_F32, T, w.out_features,
+            w.in_features, w.group_size, int(w.has_zeros), self._st()), "sf_q4_gemv_fused_rows")
+
     def _rows_forward(self, b, T, dev_pos: bool):
         """Embed b["ids"][:T], run every layer over the T rows at positions
         pos.. (host `self.pos`, or pos_dev when dev_pos: graph-replayable) and
-        leave the final-normed rows in b["Xn"][:T]."""
+        leave the final-normed rows in b["Xn"][:T]. `_rows_plan(T)` says
+        where the residual is added and which norms / SwiGLU fold into the
+        next projection; every combination gives the same bits."""
         Hb, Xn, QKV, Q, A, Dl, GU, ACT = (b[k][:T] for k in ("H", "Xn", "QKV", "Q", "A", "Dl", "GU", "ACT"))
         lib, st = self.lib, self._st()
         self._chk(lib.sf_embed(b["ids"].data_ptr(), self.embed.data_ptr(), _lib.SF_BF16, Hb.data_ptr(),
                                T, self.H, self.V, st), "sf_embed")
         pos_dev = self.pos_dev.data_ptr() if dev_pos else None
+        res, fq, fg, fd = self._rows_plan(T)
+        RMS, SILU = _lib.SF_PRE_RMSNORM, _lib.SF_PRE_SILU_MUL
+        # without the residual inside the projections, each norm adds the
+        # previous projection's output (Dl) to the residual rows itself
+        delta = lambda l: None if res or l < 0 else Dl
         for l, L in enumerate(self.layers):
-            self._rmsnorm(Hb, None if l == 0 else Dl, L.w_in, Xn, T)
-            self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
+            if fq:
+                self._gemv_fused_rows(L.qkv, Hb, RMS, L.w_in, QKV, L.qkv_bias, T)
+            else:
+                self._rmsnorm(Hb, delta(l - 1), L.w_in, Xn, T)
+                self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
             self._rope_append(l, QKV, Q, T, pos_dev, 0 if dev_pos else self.pos)
             args = (Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
                     self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, A.data_ptr(),
@@ -460,13 +496,25 @@ class LlamaModel:
             else:
                 self._chk(lib.sf_attn_prefill_i8kv(*args, T, self.Hq, self.KVH, self.pos, self.max_seq,
                                                    self.D, self.scale, st), "sf_attn_prefill_i8kv")
-            self._gemm(L.o, A, Dl, None)
-            self._rmsnorm(Hb, Dl, L.w_post, Xn, T)
-            self._gemm(L.gate_up, Xn, GU, None)
+            if res:
+                self._gemm(L.o, A, Hb, Hb)  # residual add as the bias (per row)
+            else:
+                self._gemm(L.o, A, Dl, None)
+            if fg:
+                self._gemv_fused_rows(L.gate_up, Hb, RMS, L.w_post, GU, None, T)
+            else:
+                self._rmsnorm(Hb, delta(l), L.w_post, Xn, T)
+                self._gemm(L.gate_up, Xn, GU, None)
+            if fd:
+                self._gemv_fused_rows(L.down, GU, SILU, None, Hb, Hb, T)
+                continue
             self._chk(lib.sf_silu_mul(GU.data_ptr(), ACT.data_ptr(), _DT[ACT.dtype], T, self.I, st),
                       "sf_silu_mul")
-            self._gemm(L.down, ACT, Dl, None)
-        self._rmsnorm(Hb, Dl, self.norm_w, Xn, T)
+            if res:
+                self._gemm(L.down, ACT, Hb, Hb)
+            else:
+                self._gemm(L.down, ACT, Dl, None)
+        self._rmsnorm(Hb, delta(len(self.layers) - 1), self.norm_w, Xn, T)
 
     # ---------------------------------------------------------------- decode
     def decode_step(self, logits: bool = False) -> None:

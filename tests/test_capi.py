@@ -147,3 +147,27 @@ def test_lm_head_rows_validation_and_sizes():
     assert lib.sf_lm_head_argmax_rows(*args(_lib.SF_F16, 896, 8, wsb=1024)) == -1
     assert "workspace too small" in _lib.last_error()
     assert lib.sf_lm_head_argmax_rows(*args(7, 896, 2)) == -1
+
+
+def test_fused_rows_support_and_validation():
+    lib = _lib.load()
+    F16, F32, RMS, SILU = _lib.SF_F16, _lib.SF_F32, _lib.SF_PRE_RMSNORM, _lib.SF_PRE_SILU_MUL
+    ok = lib.sf_q4_gemv_fused_rows_supported
+    # config-5 verify shapes: the two RMSNorm folds run at 3..8 rows in fp16;
+    # the down projection's plan (8 blocks per wave) keeps its SwiGLU separate;
+    # one row always folds
+    for B in (1, 3, 5, 8):
+        assert ok(RMS, B, 1152, 896, 64, 0, F16) == 1
+        assert ok(RMS, B, 9728, 896, 64, 0, F16) == 1
+        assert ok(SILU, B, 896, 4864, 64, 0, F16) == (B == 1)
+    assert ok(SILU, 4, 1152, 896, 64, 0, F16) == 1         # two blocks per wave: folds
+    assert ok(RMS, 2, 1152, 896, 64, 0, F16) == 0          # two rows: the VALU GEMV, unfolded
+    assert ok(RMS, 4, 1152, 896, 64, 0, F32) == 0          # fp32 activations
+    assert ok(RMS, 1, 1152, 896, 64, 0, F32) == 1
+    assert ok(7, 4, 1152, 896, 64, 0, F16) == 0
+    blob, src, y = 256 * 1024, 4096, 8192  # fake addresses: validation fails before any use
+    args = lambda B, K=896: (blob, src, RMS, src, 1e-6, F16, None, F32, y, None, F32, B, 1152, K,
+                             64, 0, None)
+    assert lib.sf_q4_gemv_fused_rows(*args(9)) == -1
+    assert lib.sf_q4_gemv_fused_rows(*args(2)) == -2
+    assert "run sf_rmsnorm" in _lib.last_error()

@@ -174,3 +174,84 @@ def test_many_rows_round_like_the_unfolded_path(dev, act):
         torch.cuda.synchronize()
         assert torch.equal(l0, l1), f"lm_head row {r}"
         assert torch.equal(y0, y1), f"gemv row {r}"
+
+
+# ------------------------------------------------------------------ batch rows
+def gemv_rows(lib, w, x, y32, bias=None):
+    B = x.shape[0]
+    _lib.check(lib.sf_q4_gemv(w.blob.data_ptr(), x.data_ptr(), _lib.dt(x), None, F32, y32.data_ptr(),
+                              None if bias is None else bias.data_ptr(), F32, B, w.out_features,
+                              w.in_features, w.group_size, int(w.has_zeros), st()), "sf_q4_gemv")
+
+
+def fused_rows(lib, w, src, op, norm_w, B, y32, bias=None, eps=1e-6):
+    _lib.check(lib.sf_q4_gemv_fused_rows(
+        w.blob.data_ptr(), src.data_ptr(), op, None if norm_w is None else norm_w.data_ptr(), eps,
+        F16, None, F32, y32.data_ptr(), None if bias is None else bias.data_ptr(), F32, B,
+        w.out_features, w.in_features, w.group_size, int(w.has_zeros), st()), "sf_q4_gemv_fused_rows")
+
+
+# config-5 verify shapes (qkv, gate_up with four tiles per wave, down) and 7B ones
+ROW_SHAPES = [(1152, 896, 64, False), (9728, 896, 64, True), (896, 4864, 64, False),
+              (4096, 4096, 128, False), (11008, 4096, 128, True), (96, 4096, 128, False)]
+
+
+@pytest.mark.parametrize("B", [3, 5, 8])
+@pytest.mark.parametrize("N,K,g,asym", ROW_SHAPES)
+@pytest.mark.parametrize("op", [_lib.SF_PRE_RMSNORM, _lib.SF_PRE_SILU_MUL])
+def test_fused_rows_equal_separate_kernels(dev, B, N, K, g, asym, op):
+    """sf_q4_gemv_fused_rows == sf_rmsnorm / sf_silu_mul then sf_q4_gemv, bit
+    for bit, with an [N] bias and with the per-row residual (bias = y_f32)."""
+    lib = _lib.load()
+    if not lib.sf_q4_gemv_fused_rows_supported(op, B, N, K, g, int(asym), F16):
+        pytest.skip("plan outside the folded kernels' range (separate kernels run instead)")
+    w, pk, s, z = make_weight(dev, N, K, g, asym, N + K + B)
+    rng = np.random.default_rng(N * B + op)
+    rms = op == _lib.SF_PRE_RMSNORM
+    src = torch.as_tensor(rng.normal(0, 2, (B, K if rms else 2 * K)).astype(np.float32)).to(dev)
+    nw = torch.as_tensor(rng.normal(1, 0.1, K).astype(np.float32)).to(dev) if rms else None
+    bias = torch.as_tensor(rng.normal(0, 1, N).astype(np.float32)).to(dev)
+    xn = torch.empty((B, K), dtype=torch.float16, device=dev)
+    if rms:
+        _lib.check(lib.sf_rmsnorm(src.data_ptr(), None, nw.data_ptr(), F32, xn.data_ptr(), F16, B, K,
+                                  1e-6, st()), "sf_rmsnorm")
+    else:
+        _lib.check(lib.sf_silu_mul(src.data_ptr(), xn.data_ptr(), F16, B, K, st()), "sf_silu_mul")
+    ref = torch.empty((B, N), device=dev)
+    got = torch.empty((B, N), device=dev)
+    gemv_rows(lib, w, xn, ref, bias)
+    fused_rows(lib, w, src, op, nw, B, got, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    # per-row residual: y = y_old + W x, each row its own y_old
+    old = torch.as_tensor(rng.normal(0, 1, (B, N)).astype(np.float32)).to(dev)
+    ref2, got2 = old.clone(), old.clone()
+    gemv_rows(lib, w, xn, ref2, ref2)
+    fused_rows(lib, w, src, op, nw, B, got2, got2)
+    torch.cuda.synchronize()
+    assert torch.equal(got2, ref2)
+    plain = torch.empty((B, N), device=dev)
+    gemv_rows(lib, w, xn, plain)
+    torch.cuda.synchronize()
+    assert torch.equal(ref2, plain + old)
+    # and the oracle on the rounded activations
+    exp = linear.gemv(pk, s.astype(np.float16).astype(np.float64),
+                      xn.float().cpu().numpy().astype(np.float64), g, zeros=z) + bias.cpu().numpy()
+    linear.assert_close(got.cpu().numpy(), exp, 1e-3, f"fused rows op={op} B={B}")
+
+
+@pytest.mark.parametrize("B", [1, 2, 4])
+def test_residual_bias_alias_valu_and_fp32(dev, B):
+    """bias = y_f32 on the VALU GEMV (batch 1-2, and fp32 activations in
+    slices of two rows) adds each row's own previous value."""
+    lib = _lib.load()
+    w, *_ = make_weight(dev, 640, 512, 64, False, 7)
+    for xdt in (torch.float16, torch.float32):
+        x = torch.randn((B, 512), device=dev).to(xdt)
+        old = torch.randn((B, 640), device=dev)
+        y = old.clone()
+        plain = torch.empty((B, 640), device=dev)
+        gemv_rows(lib, w, x, y, y)
+        gemv_rows(lib, w, x, plain)
+        torch.cuda.synchronize()
+        assert torch.equal(y, plain + old), f"{xdt} B={B}"

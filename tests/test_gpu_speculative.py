@@ -49,7 +49,15 @@ def near_tie(logits: np.ndarray, a: int, b: int, tol: float) -> bool:
 ROW_CASES = [(1000, 256, 8, torch.float32), (1000, 256, 3, torch.float16),
              (5003, 896, 8, torch.bfloat16), (5003, 896, 1, torch.float32),
              (151936, 896, 8, torch.float16), (4099, 4096, 8, torch.bfloat16),
-             (4099, 4096, 4, torch.float32), (777, 8192, 2, torch.float16)]
+             (4099, 4096, 4, torch.float32), (777, 8192, 2, torch.float16),
+             (3001, 2048, 8, torch.float16), (2000, 1536, 5, torch.bfloat16),
+             (1000, 904, 4, torch.float16), (1000, 896, 2, torch.float16),
+             (1000, 896, 3, torch.float16)]
+
+
+def rows_on_mfma(H, B, xdt):
+    """From 3 rows, fp16 / bf16 rows with H % 32 == 0 and H <= 2048 run on MFMA."""
+    return B >= 3 and xdt != torch.float32 and H % 32 == 0 and H <= 2048
 
 
 @pytest.mark.parametrize("V,H,B,xdt", ROW_CASES)
@@ -77,9 +85,18 @@ def test_lm_head_rows_equal_single_row(dev, V, H, B, xdt):
                                          V, H, one_t.data_ptr(), None, None, ws1.data_ptr(),
                                          ws1.numel(), st()), "sf_lm_head_argmax")
         torch.cuda.synchronize()
-        assert torch.equal(logits[b], one_l), f"row {b}: logits differ from the single-row kernel"
-        assert int(toks[b]) == int(one_t[0]) == int(np.argmax(lg[b])), f"row {b}: token"
+        assert int(toks[b]) == int(np.argmax(lg[b])), f"row {b}: token is not its logits' argmax"
         np.testing.assert_allclose(lg[b], ref[b], rtol=0, atol=1e-5 * np.abs(ref[b]).max() + 1e-6)
+        if not rows_on_mfma(H, B, xdt):
+            # the VALU kernel sums each row in the single-row kernel's order
+            assert torch.equal(logits[b], one_l), f"row {b}: logits differ from the single-row kernel"
+            assert int(toks[b]) == int(one_t[0]), f"row {b}: token"
+        else:
+            # MFMA: exact products, fp32 sums in another order
+            one = one_l.cpu().numpy()
+            np.testing.assert_allclose(lg[b], one, rtol=0, atol=2e-6 * np.abs(one).max())
+            if int(toks[b]) != int(one_t[0]):
+                assert near_tie(one, int(toks[b]), int(one_t[0]), 1e-5), f"row {b}: token"
     assert int(toks[0]) == int(toks[B - 1])
     # without logits: the same tokens
     toks2 = torch.full((B,), -1, dtype=torch.int32, device=dev)
@@ -169,6 +186,30 @@ def test_verify_graph_equals_eager(dev, max_seq, prompt_len):
         # trim back one row each time: the next verify overwrites it
         g.set_position(n - 1)
         e.set_position(n - 1)
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 5, 8])
+def test_fused_verify_equals_unfused(dev, B):
+    """The verify forward with RMSNorm / SwiGLU folded into the batch GEMV and
+    the residual added inside the o / down projections gives the same bits as
+    the separate kernels (LlamaModel(fuse=False)), fp16 activations."""
+    outs = []
+    for fuse in (True, False):
+        m = LlamaModel.random_init(SMALL, seed=47, group_size=64, device=dev, max_seq=64,
+                                   act_dtype=torch.float16, fuse=fuse)
+        g = torch.Generator(device=dev).manual_seed(3)
+        for L in m.layers:  # non-unit norm weights
+            L.w_in.mul_(1 + 0.2 * torch.randn(L.w_in.shape, generator=g, device=dev))
+            L.w_post.mul_(1 + 0.2 * torch.randn(L.w_post.shape, generator=g, device=dev))
+        res, fq, fg, fd = m._rows_plan(B)
+        assert res and fq == fg == (fuse and B != 2)
+        rng = np.random.default_rng(48)
+        m.reset()
+        m.prefill(rng.integers(0, SMALL.vocab_size, 11))
+        toks = m.verify(rng.integers(0, SMALL.vocab_size, B), want_logits=True)
+        outs.append((toks, m.vlogits[:B].cpu().clone(), m.k_codes[1][:, :m.pos].cpu().clone()))
+    (t0, l0, k0), (t1, l1, k1) = outs
+    assert t0 == t1 and torch.equal(l0, l1) and torch.equal(k0, k1)
 
 
 def test_trim_discards_stale_rows(dev):
