@@ -6,29 +6,30 @@
 // GEMV over the T rows and re-stream W for each; here W is read once per
 // 128-row block of X.
 //
-// Exactness without a per-group epilogue: with an fp16 scale, the dequantized
-// weight w = (q - z) * s has at most 15 significant bits, so it is exactly
-// w_hi + w_lo with w_hi = w truncated to bf16 (8 bits) and w_lo = w - w_hi (at
-// most 7 bits, also exact in bf16). The workgroup dequantizes its W tile once
-// into LDS as these two bf16 tiles, and every wave runs
-// v_mfma_f32_32x32x16_bf16 on X*W_hi + X*W_lo. bf16 activations are exact
-// operands; fp16 / fp32 activations are split the same way into bf16 hi + lo
-// (fp16 exactly, fp32 to ~16 bits) and all four products are accumulated, so
-// fp16 activations give exact products like the bf16 ones.
+// Exact products, scale per group: the workgroup dequantizes its W tile once
+// into LDS as the integers q - z (|q - z| <= 15, exact in fp16 and in bf16)
+// and every wave runs one MFMA per product on them — v_mfma_f32_32x32x16_f16
+// for fp16 activations, _bf16 for bf16 ones (fp32 activations are split into
+// bf16 high and low parts, two MFMAs) — accumulating each scale group's
+// partial in fp32 and folding it into the result with the group's fp16 scale,
+// once per group: y = sum_g s_g * sum_{k in g} x_k (q_k - z), the reference's
+// own grouping (q4_gemv.cpp:136). Each staging thread writes its row's scale
+// into a small LDS table beside the W tile; a lane reads its column's.
 //
 // Tiling: 128 x 128 output tile per 512-thread workgroup (2 x 4 waves, each
 // 64 x 32 = 2 MFMA 32x32 tiles; two waves per SIMD), K steps of 64 staged
-// through two padded LDS buffers; each step's global loads are issued three
-// steps ahead (a ring of three register stages) so HBM latency hides behind
-// the MFMAs. The output tile goes back through LDS so that stores are whole
-// row segments. When
-// the tile grid is too small to fill the GPU, K is split across workgroups
-// into an fp32 workspace and summed by a second kernel in a fixed order.
+// through two padded LDS buffers (74 KB: two workgroups fit a CU); each
+// step's global loads are issued three steps ahead (a ring of three register
+// stages) so HBM latency hides behind the MFMAs. The output tile goes back
+// through LDS so that stores are whole row segments. When the tile grid is
+// too small to fill the GPU, K is split across workgroups into an fp32
+// workspace and summed by a second kernel in a fixed order.
 #include "sf_common.h"
 
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
@@ -76,13 +77,14 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
   lo = hi_pair(sf_bitcast<uint32_t>(ra), sf_bitcast<uint32_t>(rb));
 }
 
-// Write the thread's KPT activations to the LDS tiles (hi only for bf16).
+// Write the thread's KPT activations to the LDS tiles: fp16 / bf16 as they
+// are, fp32 as bf16 high and low parts.
 template <int XDT>
 __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, uint16_t *xs_lo,
                                         int lrow, int lk) {
   u32x4 *dh = (u32x4 *)(xs_hi + lrow * LDS_PITCH + lk);
   const uint32_t keep = r.ok ? 0xFFFFFFFFu : 0u;
-  if constexpr (XDT == SF_BF16) {
+  if constexpr (XDT != SF_F32) {
 #pragma unroll
     for (int i = 0; i < KPT / 8; ++i) dh[i] = r.v[i] & keep;
   } else {
@@ -90,17 +92,8 @@ __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, ui
 #pragma unroll
     for (int i = 0; i < KPT / 8; ++i) {  // 8 activations per 16-byte LDS store
       float f[8];
-      if constexpr (XDT == SF_F16) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const half2_t h = sf_bitcast<half2_t>(r.v[i][j] & keep);
-          f[2 * j] = (float)h.x;
-          f[2 * j + 1] = (float)h.y;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = sf_bitcast<float>(r.v[2 * i + j / 4][j % 4] & keep);
-      }
+      for (int j = 0; j < 8; ++j) f[j] = sf_bitcast<float>(r.v[2 * i + j / 4][j % 4] & keep);
       u32x4 h4, l4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -137,39 +130,40 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *__restrict__ wq,
   if constexpr (ASYM) r.zbyte = zt[cell * 4 + ((nc & 7) >> 1)];
 }
 
-// Dequantize KPT weights exactly and store them as bf16 hi / lo LDS rows.
-template <bool ASYM>
-__device__ __forceinline__ void store_w(const WRegs &r, uint16_t *ws_hi, uint16_t *ws_lo, int lrow,
+// Store the thread's KPT weights as the integers q - z (fp16 when MT is
+// SF_F16, else bf16; zero past the matrix) and, from the threads at the start
+// of a 32-k half, the row's scale for that half into the scale table.
+template <bool ASYM, int MT>
+__device__ __forceinline__ void store_w(const WRegs &r, uint16_t *ws, uint16_t *ss, int lrow,
                                         int lk) {
-  u32x4 *dh = (u32x4 *)(ws_hi + lrow * LDS_PITCH + lk);
-  u32x4 *dl = (u32x4 *)(ws_lo + lrow * LDS_PITCH + lk);
+  u32x4 *d = (u32x4 *)(ws + lrow * LDS_PITCH + lk);
   // row n's zero-point nibble: the low one for even n, the high one for odd n
   // (offset-binary symmetric codes have z = 8)
   uint32_t z = 8u;
   if constexpr (ASYM) z = (r.zbyte >> (4 * (lrow & 1))) & 15u;
-  const float sc = r.ok ? (float)sf_bitcast<f16>((uint16_t)r.sbits) : 0.f;
-  const float zs = (float)z * sc;
+  const uint32_t keep = r.ok ? 0xFFFFFFFFu : 0u;
 #pragma unroll
   for (int i = 0; i < KPT / 8; ++i) {  // dword i holds k = 8i .. 8i+7
-    const uint32_t d = i == 0 ? r.w.x : r.w.y;
-    const uint32_t lo4 = d & 0x0F0F0F0Fu, hi4 = (d >> 4) & 0x0F0F0F0Fu;
-    float v[8];
+    const uint32_t dw = i == 0 ? r.w.x : r.w.y;
+    const uint32_t lo4 = dw & 0x0F0F0F0Fu, hi4 = (dw >> 4) & 0x0F0F0F0Fu;
+    u32x4 o;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      v[2 * b] = fmaf((float)((lo4 >> (8 * b)) & 0xFFu), sc, -zs);      // k = 8i + 2b
-      v[2 * b + 1] = fmaf((float)((hi4 >> (8 * b)) & 0xFFu), sc, -zs);  // k = 8i + 2b + 1
+    for (int b = 0; b < 4; ++b) {  // pair (k = 8i + 2b, 8i + 2b + 1) = byte b of lo4 / hi4
+      // byte b of lo4 -> bits 0..7, byte b of hi4 -> bits 16..23
+      const uint32_t pq = __builtin_amdgcn_perm(hi4, lo4, 0x0c000c00u | ((4u + b) << 16) | b);
+      if constexpr (MT == SF_F16) {
+        // 1024 + q as fp16, minus (1024 + z): exact
+        const half2_t v = sf_bitcast<half2_t>(pq | 0x64006400u) +
+                          sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);
+        o[b] = sf_bitcast<uint32_t>(v);
+      } else {
+        const float f0 = (float)(int)((pq & 0xFFu) - z), f1 = (float)(int)((pq >> 16) - z);
+        o[b] = hi_pair(sf_bitcast<uint32_t>(f0), sf_bitcast<uint32_t>(f1));
+      }
     }
-    u32x4 h4, l4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t hp, lp;
-      split2(v[2 * j], v[2 * j + 1], hp, lp);
-      h4[j] = hp;
-      l4[j] = lp;
-    }
-    dh[i] = h4;
-    dl[i] = l4;
+    d[i] = o & keep;
   }
+  if ((lk & 31) == 0) ss[lrow * 2 + (lk >> 5)] = (uint16_t)r.sbits;
 }
 
 // Write 8 consecutive outputs (nv of them in range) to the fp32 copy and / or
@@ -211,23 +205,29 @@ __device__ __forceinline__ void store_row8(const float (&v)[8], int nv, bool vec
   }
 }
 
-template <int XDT, bool ASYM>
-__global__ void __launch_bounds__(NTHREADS, 1)
+// GK: the group size's shape, fixed at compile time so the per-group folds
+// are straight-line code: 0 = 32 (two groups per K step), 1 = 64 (one per
+// step), 2 = a multiple of 128 (a group spans several steps; a test per
+// step), 3 = any other multiple of 32 (a test per 16-k slice).
+template <int XDT, bool ASYM, int GK>
+__global__ void __launch_bounds__(NTHREADS, 2)
 k_q4_gemm(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
           const uint8_t *__restrict__ zt, const void *__restrict__ X, void *__restrict__ Y,
           int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt,
           float *__restrict__ part, int M, int N, int K, int G, int g, int ksplit,
           int steps_per_split, bool vec) {
-  constexpr bool XSPLIT = XDT != SF_BF16;
+  constexpr bool XSPLIT = XDT == SF_F32;             // fp32 activations: bf16 hi + lo
+  constexpr int MT = XDT == SF_F16 ? SF_F16 : SF_BF16;  // MFMA operand type
   constexpr int XB = BM * LDS_PITCH, WB = BN * LDS_PITCH;  // one LDS buffer of each tile
-  constexpr int SMEM_U16 = 2 * XB * (XSPLIT ? 2 : 1) + 4 * WB;
+  constexpr int SB = BN * 2;                               // scales: 2 halves of the step per row
+  constexpr int SMEM_U16 = 2 * XB * (XSPLIT ? 2 : 1) + 2 * WB + 2 * SB;
   constexpr int NWAVES = NTHREADS / 64;
-  static_assert(SMEM_U16 * 2 >= NWAVES * WAVE_M * OUT_PITCH * 4, "output staging must fit");
-  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_U16];
+  constexpr int OUT_U16 = NWAVES * WAVE_M * OUT_PITCH * 2;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_U16 > OUT_U16 ? SMEM_U16 : OUT_U16];
   uint16_t *const xs_hi = smem;
   uint16_t *const xs_lo = smem + 2 * XB;  // used only when XSPLIT
-  uint16_t *const ws_hi = smem + 2 * XB * (XSPLIT ? 2 : 1);
-  uint16_t *const ws_lo = ws_hi + 2 * WB;
+  uint16_t *const ws = smem + 2 * XB * (XSPLIT ? 2 : 1);
+  uint16_t *const ss = ws + 2 * WB;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -242,11 +242,11 @@ k_q4_gemm(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // staging assignment: row tid / (BK / KPT), KPT consecutive k
   const int lrow = tid / (BK / KPT), lk = (tid % (BK / KPT)) * KPT;
 
-  float16_t acc[2];
+  float16_t acc[2], gp[2];  // the result, and the current scale group's partial
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[i][r] = gp[i][r] = 0.f;
 
   // Loads past the split's last step re-read that step (in bounds, unused), so
   // every load is unconditional and stays in flight.
@@ -258,34 +258,73 @@ k_q4_gemm(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   auto store = [&](int step, const XRegs<XDT> &xr, const WRegs &wr) {
     const int b = step & 1;
     store_x<XDT>(xr, xs_hi + b * XB, xs_lo + (XSPLIT ? b * XB : 0), lrow, lk);
-    store_w<ASYM>(wr, ws_hi + b * WB, ws_lo + b * WB, lrow, lk);
+    store_w<ASYM, MT>(wr, ws + b * WB, ss + b * SB, lrow, lk);
   };
-  auto compute = [&](int step) {
+  // a lane's accumulators all belong to output column c: one scale per group
+  auto fold = [&](float sc) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = fmaf(gp[i][r], sc, acc[i][r]);
+  };
+  const float16_t zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
+                            0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // one K step; `fresh`: the step starts a scale group (its first MFMAs take
+  // a zero accumulator), `last`: the step ends one (fold after it)
+  auto compute_step = [&](int step, bool fresh, bool last) {
     const int b = step & 1;
     const uint16_t *xh = xs_hi + b * XB, *xl = xs_lo + (XSPLIT ? b * XB : 0);
-    const uint16_t *wh = ws_hi + b * WB, *wl = ws_lo + b * WB;
+    const uint16_t *wt = ws + b * WB;
     const int c = wn + (lane & 31);
+    const int kb = step * BK;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
+      // a group starts here: the slice's MFMAs take a zero accumulator
+      const bool zc = GK == 3 ? (kk % 32 == 0 && ((kb + kk) % g == 0 || (kk == 0 && step == s0)))
+                              : (kk == 0 && fresh) || (GK == 0 && kk == 32);
       const int kofs = kk + (lane >> 5) * 8;
-      bf16x8_t ah[2], al[2];
+      u32x4 ah[2], al[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int r = wm + i * 32 + (lane & 31);
-        ah[i] = *(const bf16x8_t *)(xh + r * LDS_PITCH + kofs);
-        if constexpr (XSPLIT) al[i] = *(const bf16x8_t *)(xl + r * LDS_PITCH + kofs);
+        ah[i] = *(const u32x4 *)(xh + r * LDS_PITCH + kofs);
+        if constexpr (XSPLIT) al[i] = *(const u32x4 *)(xl + r * LDS_PITCH + kofs);
       }
-      const bf16x8_t bh = *(const bf16x8_t *)(wh + c * LDS_PITCH + kofs);
-      const bf16x8_t bl = *(const bf16x8_t *)(wl + c * LDS_PITCH + kofs);
+      const u32x4 bw = *(const u32x4 *)(wt + c * LDS_PITCH + kofs);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh, acc[i], 0, 0, 0);
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl, acc[i], 0, 0, 0);
-        if constexpr (XSPLIT) {
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh, acc[i], 0, 0, 0);
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bl, acc[i], 0, 0, 0);
+        const float16_t cin = zc ? zero16 : gp[i];
+        if constexpr (MT == SF_F16) {
+          gp[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sf_bitcast<half8_t>(ah[i]),
+                                                         sf_bitcast<half8_t>(bw), cin, 0, 0, 0);
+        } else {
+          gp[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf_bitcast<bf16x8_t>(ah[i]),
+                                                          sf_bitcast<bf16x8_t>(bw), cin, 0, 0, 0);
+          if constexpr (XSPLIT)
+            gp[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf_bitcast<bf16x8_t>(al[i]),
+                                                            sf_bitcast<bf16x8_t>(bw), gp[i], 0, 0, 0);
         }
       }
+      // a group ends after this 16-k slice: scale the partial once
+      const bool end = GK == 3 ? (kk % 32 == 16 && ((kb + kk + 16) % g == 0 ||
+                                                    (kk == BK - 16 && step == s1 - 1)))
+                               : (GK == 0 && kk == 16) || (kk == BK - 16 && last);
+      if (end) fold((float)sf_bitcast<f16>(ss[b * SB + c * 2 + (kk >> 5)]));
+    }
+  };
+  // g = 32 / 64: every step starts and ends its groups; g >= 128: a group
+  // spans g / 64 steps (and a split's last step closes its open group)
+  auto compute = [&](int step) {
+    if constexpr (GK < 2 || GK == 3) {
+      compute_step(step, true, true);  // (GK 3 decides per slice)
+    } else {
+      const int spg = g / BK;
+      const bool fresh = step % spg == 0 || step == s0;
+      const bool last = (step + 1) % spg == 0 || step == s1 - 1;
+      if (fresh && last) compute_step(step, true, true);
+      else if (fresh) compute_step(step, true, false);
+      else if (last) compute_step(step, false, true);
+      else compute_step(step, false, false);
     }
   };
 
@@ -496,10 +535,25 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
   // 16-byte output stores need rows of whole 16-byte multiples and aligned bases
   const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)y_f32 & 15) == 0 &&
                    ((uintptr_t)part & 15) == 0;
-#define SF_GEMM_LAUNCH(XD, AS)                                                                 \
-  k_q4_gemm<XD, AS><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias, bias_dtype, \
-                                              part, M, N, K, L.G, group_size, ksplit,            \
-                                              steps_per_split, vec)
+#define SF_GEMM_LAUNCH(XD, AS)                                                               \
+  do {                                                                                       \
+    if (group_size == 32)                                                                    \
+      k_q4_gemm<XD, AS, 0><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias,  \
+                                                     bias_dtype, part, M, N, K, L.G,         \
+                                                     group_size, ksplit, steps_per_split, vec); \
+    else if (group_size == 64)                                                               \
+      k_q4_gemm<XD, AS, 1><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias,  \
+                                                     bias_dtype, part, M, N, K, L.G,         \
+                                                     group_size, ksplit, steps_per_split, vec); \
+    else if (group_size % 64)                                                                \
+      k_q4_gemm<XD, AS, 3><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias,  \
+                                                     bias_dtype, part, M, N, K, L.G,         \
+                                                     group_size, ksplit, steps_per_split, vec); \
+    else                                                                                     \
+      k_q4_gemm<XD, AS, 2><<<grid, NTHREADS, 0, s>>>(w, st, zt, x, y, y_dtype, y_f32, bias,  \
+                                                     bias_dtype, part, M, N, K, L.G,         \
+                                                     group_size, ksplit, steps_per_split, vec); \
+  } while (0)
 #define SF_GEMM_X(AS)                                  \
   do {                                                 \
     if (x_dtype == SF_BF16) SF_GEMM_LAUNCH(SF_BF16, AS); \

@@ -48,7 +48,11 @@ def test_config2_asym_prefill(dev, N, K):
 
 
 @pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("M,N,K,g", [(33, 100, 256, 64), (200, 257, 512, 128), (130, 640, 96, 32)])
+@pytest.mark.parametrize("M,N,K,g", [(33, 100, 256, 64), (200, 257, 512, 128), (130, 640, 96, 32),
+                                     # groups of 96 (a group boundary inside a K step) and
+                                     # 256 (four steps); split-K starting mid-group
+                                     (130, 200, 288, 96), (70, 300, 1024, 256),
+                                     (64, 96, 1152, 128), (40, 50, 1152, 96)])
 def test_gemm_shapes_and_dtypes_sym(dev, xdtype, M, N, K, g):
     rng = np.random.default_rng(M + N + K)
     W = rng.normal(0, 1, (N, K)).astype(np.float32)
