@@ -293,8 +293,10 @@ def e2e_decode(dev, runs: int = 3):
     import torch
 
     out = {}
+    m_rope = False
     for name, act in (("fp16", torch.float16), ("fp32", torch.float32)):
         cfg, m, ids = e2e_model(dev, act)
+        m_rope = m._qkv_rope
         m.capture()
         m.generate(ids, 16)
         rs = [m.generate(ids, E2E_TOKENS) for _ in range(runs)]
@@ -322,9 +324,11 @@ def e2e_decode(dev, runs: int = 3):
         }
         del m
         torch.cuda.empty_cache()
-    # embed; per layer qkv (norm folded), rope+append, attention, o, gate_up
-    # (norm folded), down (SwiGLU folded); lm_head (final norm folded)
-    out["launches_per_token"] = 1 + 6 * cfg.num_hidden_layers + 1
+    # embed; per layer qkv (norm folded; RoPE + KV append folded into its
+    # epilogue where the plan allows), attention, o, gate_up (norm folded), down
+    # (SwiGLU folded); lm_head (final norm folded)
+    per_layer = 5 if m_rope else 6
+    out["launches_per_token"] = 1 + per_layer * cfg.num_hidden_layers + 1
     return out
 
 

@@ -119,6 +119,23 @@ int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op, const floa
                           const void *bias, int bias_dtype, int B, int N, int K, int group_size,
                           int has_zeros, void *stream);
 
+/* The decode step's qkv projection with the input RMSNorm folded into its
+ * activation load (sf_q4_gemv_fused, SF_PRE_RMSNORM) and RoPE + the KV-cache
+ * append (sf_rope_kv_append at the device position *pos_dev) folded into its
+ * epilogue: q_out [H][D] and the cache row at *pos_dev get the same bits as
+ * those two calls; the fp32 q|k|v rows are not stored. Needs one head per
+ * workgroup of the batch-1 plan (in_features <= 1024 for D = 64);
+ * sf_q4_gemv_fused_rope_supported says so (1), else SF_EUNSUPPORTED. No
+ * counterpart in the reference (layers.py:93-112 runs these as separate ops). */
+int sf_q4_gemv_fused_rope_supported(int N, int K, int group_size, int H, int KVH, int D,
+                                    int act_dtype);
+int sf_q4_gemv_fused_rope(const void *blob, const float *h, const float *norm_w, float eps,
+                          int act_dtype, const void *bias, int bias_dtype, const float *cos_t,
+                          const float *sin_t, int max_pos, void *q_out, int q_dtype,
+                          int8_t *k_codes, void *k_scales, int8_t *v_codes, void *v_scales,
+                          int scale_dtype, int H, int KVH, int D, int T_cap, const int *pos_dev,
+                          int N, int K, int group_size, int has_zeros, void *stream);
+
 /* ---- prefill GEMM (M rows) ------------------------------------------------
  * Y[m, n] = X[m, :] . dequant(W)[n, :] for M rows; replaces q4_gemm_sym /
  * q4_gemm_asym (bindings.cpp:98-150; q4_gemm.cpp:12-51). bf16/f16 MFMA on

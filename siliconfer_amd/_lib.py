@@ -40,6 +40,10 @@ _SIGS = {
     "sf_q4_gemv_fused_rows_supported": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
     "sf_q4_gemv_fused_rows": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_f, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                                      _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
+    "sf_q4_gemv_fused_rope_supported": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
+    "sf_q4_gemv_fused_rope": (_c_i, [_c_p, _c_p, _c_p, _c_f, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p,
+                                     _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                     _c_p, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_q4_gemm_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
     "sf_q4_gemm": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),

@@ -24,11 +24,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float wave_max(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
 __device__ __forceinline__ void store_as(void *p, int dt, size_t i, float v) {
   if (dt == SF_F32) ((float *)p)[i] = v;
   else if (dt == SF_F16) ((f16 *)p)[i] = (f16)v;
@@ -74,76 +69,17 @@ k_rmsnorm(float *__restrict__ x, const float *__restrict__ delta, const void *__
 
 // ---------------------------------------------------------------------------
 // One wave per (row, head) of the fused q|k|v projection output
-// qkv [rows][(H + 2 KVH) * D]. Rotate-half RoPE (layers.py:58-66):
-// out[d] = x[d] cos - x[d + D/2] sin, out[d + D/2] = x[d + D/2] cos + x[d] sin,
-// with cos / sin of (position * freq_d) from the host-made fp32 tables. q goes
-// to q_out; rotated k and raw v are quantized per (head, token) exactly as
-// sf_kv_quant_append does (s = max|x| / 127, 1 if 0; code = clip(rint(x / s)))
-// into the cache at position pos0 + row (batch 1).
-template <int QDT, int SDT>
+// qkv [rows][(H + 2 KVH) * D]: sf_rope_append_head (rotate-half RoPE with the
+// host-made fp32 cos / sin tables, q to q_out, k and v quantized per (head,
+// token) into the cache at position pos0 + row, batch 1).
 __global__ void __launch_bounds__(64)
-k_rope_kv_append(const float *__restrict__ qkv, const float *__restrict__ cos_t,
-                 const float *__restrict__ sin_t, int max_pos, void *__restrict__ q_out,
-                 int8_t *__restrict__ k_codes, void *__restrict__ k_scales,
-                 int8_t *__restrict__ v_codes, void *__restrict__ v_scales, int H, int KVH, int D,
-                 int T_cap, const int *__restrict__ pos_dev, int pos_host) {
-  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+k_rope_kv_append(const float *__restrict__ qkv, SfRopeAppend a, const int *__restrict__ pos_dev,
+                 int pos_host) {
+  const int row = blockIdx.x, head = blockIdx.y;
   const int pos = (pos_dev ? *pos_dev : pos_host) + row;
-  const int half = D >> 1;
-  const int width = (H + 2 * KVH) * D;
-  const float *x = qkv + (size_t)row * width + (size_t)head * D;
-  const bool is_q = head < H, is_k = !is_q && head < H + KVH;
-  if (pos < 0 || pos >= T_cap || pos >= max_pos) return;  // the host keeps positions in range
-  // each lane owns the dimension pairs (d, d + D/2) for d = lane, lane + 64, ...
-  constexpr int MAXP = 2;  // D <= 256
-  float lo[MAXP], hi[MAXP];
-#pragma unroll
-  for (int j = 0; j < MAXP; ++j) {
-    const int d = lane + 64 * j;
-    lo[j] = hi[j] = 0.f;
-    if (d < half) {
-      const float a = x[d], b = x[d + half];
-      if (is_q || is_k) {
-        // separately rounded products, as x * cos + rotate(x) * sin in fp32
-#pragma clang fp contract(off)
-        const float c = cos_t[(size_t)pos * half + d], s = sin_t[(size_t)pos * half + d];
-        lo[j] = a * c - b * s;
-        hi[j] = b * c + a * s;
-      } else {
-        lo[j] = a;
-        hi[j] = b;
-      }
-    }
-  }
-  if (is_q) {
-#pragma unroll
-    for (int j = 0; j < MAXP; ++j) {
-      const int d = lane + 64 * j;
-      if (d < half) {
-        const size_t o = ((size_t)row * H + head) * D + d;
-        sf_store_from_f32<QDT>(q_out, o, lo[j]);
-        sf_store_from_f32<QDT>(q_out, o + half, hi[j]);
-      }
-    }
-    return;
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int j = 0; j < MAXP; ++j) amax = fmaxf(amax, fmaxf(fabsf(lo[j]), fabsf(hi[j])));
-  amax = wave_max(amax);
-  const float s = amax == 0.f ? 1.f : amax / 127.f;
-  const int kvh = is_k ? head - H : head - H - KVH;
-  const size_t crow = (size_t)kvh * T_cap + pos;
-  int8_t *codes = (is_k ? k_codes : v_codes) + crow * D;
-#pragma unroll
-  for (int j = 0; j < MAXP; ++j) {
-    const int d = lane + 64 * j;
-    if (d < half) {
-      codes[d] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(lo[j] / s), -128.f), 127.f);
-      codes[d + half] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(hi[j] / s), -128.f), 127.f);
-    }
-  }
-  if (lane == 0) sf_store_from_f32<SDT>(is_k ? k_scales : v_scales, crow, s);
+  if (pos < 0 || pos >= a.T_cap || pos >= a.max_pos) return;  // the host keeps positions in range
+  const int width = (a.H + 2 * a.KVH) * a.D;
+  sf_rope_append_head(a, qkv + (size_t)row * width + (size_t)head * a.D, head, pos, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -678,21 +614,9 @@ extern "C" int sf_rope_kv_append(const float *qkv, const float *cos_t, const flo
                "positions %d..%d exceed the cache capacity %d or the RoPE table %d", pos_host,
                pos_host + rows - 1, T_cap, max_pos);
   dim3 grid(rows, H + 2 * KVH);
-  hipStream_t st = (hipStream_t)stream;
-#define SF_ROPE_LAUNCH(QD, SD)                                                                    \
-  k_rope_kv_append<QD, SD><<<grid, 64, 0, st>>>(qkv, cos_t, sin_t, max_pos, q_out, k_codes,        \
-                                                 k_scales, v_codes, v_scales, H, KVH, D, T_cap,    \
-                                                 pos_dev, pos_host)
-  if (scale_dtype == SF_F16) {
-    if (q_dtype == SF_F32) SF_ROPE_LAUNCH(SF_F32, SF_F16);
-    else if (q_dtype == SF_F16) SF_ROPE_LAUNCH(SF_F16, SF_F16);
-    else SF_ROPE_LAUNCH(SF_BF16, SF_F16);
-  } else {
-    if (q_dtype == SF_F32) SF_ROPE_LAUNCH(SF_F32, SF_F32);
-    else if (q_dtype == SF_F16) SF_ROPE_LAUNCH(SF_F16, SF_F32);
-    else SF_ROPE_LAUNCH(SF_BF16, SF_F32);
-  }
-#undef SF_ROPE_LAUNCH
+  const SfRopeAppend a{cos_t, sin_t, max_pos, q_out, q_dtype, k_codes, k_scales, v_codes,
+                       v_scales, scale_dtype, H, KVH, D, T_cap};
+  k_rope_kv_append<<<grid, 64, 0, (hipStream_t)stream>>>(qkv, a, pos_dev, pos_host);
   return sf_check_launch("sf_rope_kv_append");
 }
 

@@ -18,7 +18,7 @@
 //
 // Tiling: 128 x 128 output tile per 512-thread workgroup (2 x 4 waves, each
 // 64 x 32 = 2 MFMA 32x32 tiles; two waves per SIMD), K steps of 64 staged
-// through two padded LDS buffers (74 KB: two workgroups fit a CU); each
+// through two padded LDS buffers (74 KB); each
 // step's global loads are issued three steps ahead (a ring of three register
 // stages) so HBM latency hides behind the MFMAs. The output tile goes back
 // through LDS so that stores are whole row segments. When the tile grid is

@@ -11,6 +11,12 @@ extern template void launch_x<SF_F32>(const GemvPlan &, const GemvArgs &);
 extern template void launch_pre<SF_F16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
 extern template void launch_pre<SF_BF16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
 extern template void launch_pre<SF_F32>(const GemvPlan &, const GemvArgs &, int, const float *, float);
+extern template void launch_pre_rope<SF_F16>(const GemvPlan &, const GemvArgs &, const float *, float,
+                                             const SfRopeAppend &, const int *);
+extern template void launch_pre_rope<SF_BF16>(const GemvPlan &, const GemvArgs &, const float *,
+                                              float, const SfRopeAppend &, const int *);
+extern template void launch_pre_rope<SF_F32>(const GemvPlan &, const GemvArgs &, const float *, float,
+                                             const SfRopeAppend &, const int *);
 }  // namespace sf_gemv
 
 using namespace sf_gemv;
@@ -163,4 +169,59 @@ extern "C" int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op,
                 (hipStream_t)stream};
   launch_mfma_gemv(args, group_size, op == SF_PRE_RMSNORM ? PRE_RMSNORM : PRE_SILU, norm_w, eps);
   return sf_check_launch("sf_q4_gemv_fused_rows");
+}
+
+extern "C" int sf_q4_gemv_fused_rope_supported(int N, int K, int group_size, int H, int KVH, int D,
+                                               int act_dtype) {
+  if (N <= 0 || K <= 0 || group_size <= 0 || K % group_size || group_size % 32 || H <= 0 ||
+      KVH <= 0 || D <= 0 || D % 2 || D > 256 || N != (H + 2 * KVH) * D || K % 32 ||
+      (act_dtype != SF_F16 && act_dtype != SF_BF16 && act_dtype != SF_F32))
+    return 0;
+  GemvPlan pl;
+  if (plan_gemv(1, N, K, group_size, act_dtype, &pl, 8)) return 0;
+  return pl.Q == 32 && pl.P == 32 && pl.RS * pl.R == D;
+}
+
+extern "C" int sf_q4_gemv_fused_rope(const void *blob, const float *h, const float *norm_w,
+                                     float eps, int act_dtype, const void *bias, int bias_dtype,
+                                     const float *cos_t, const float *sin_t, int max_pos,
+                                     void *q_out, int q_dtype, int8_t *k_codes, void *k_scales,
+                                     int8_t *v_codes, void *v_scales, int scale_dtype, int H,
+                                     int KVH, int D, int T_cap, const int *pos_dev, int N, int K,
+                                     int group_size, int has_zeros, void *stream) {
+  SF_REQUIRE(blob && h && norm_w && cos_t && sin_t && q_out && k_codes && k_scales && v_codes &&
+                 v_scales && pos_dev,
+             SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(q_dtype >= SF_F32 && q_dtype <= SF_BF16, SF_EINVAL, "bad q dtype %d", q_dtype);
+  SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
+             scale_dtype);
+  SF_REQUIRE(!bias || bias_dtype == SF_F16 || bias_dtype == SF_BF16 || bias_dtype == SF_F32,
+             SF_EINVAL, "bad bias dtype %d", bias_dtype);
+  SF_REQUIRE(T_cap > 0 && max_pos > 0, SF_EINVAL, "invalid cache capacity %d / RoPE table %d",
+             T_cap, max_pos);
+  SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)h & 15) == 0 &&
+                 ((uintptr_t)norm_w & 15) == 0,
+             SF_EINVAL, "blob must be 256-byte aligned, h and norm_w 16-byte aligned");
+  SF_REQUIRE(sf_q4_gemv_fused_rope_supported(N, K, group_size, H, KVH, D, act_dtype),
+             SF_EUNSUPPORTED,
+             "qkv projection N=%d K=%d group_size=%d heads %d/%d x %d: the folded RoPE needs one "
+             "head per workgroup of the batch-1 plan (in_features <= 1024); run sf_q4_gemv_fused "
+             "and sf_rope_kv_append instead",
+             N, K, group_size, H, KVH, D);
+  BlobLayout L;
+  sf_blob_layout(N, K, group_size, has_zeros, &L);
+  GemvPlan pl;
+  int rc = plan_gemv(1, N, K, group_size, act_dtype, &pl, 8);
+  if (rc) return rc;
+  const uint8_t *w = (const uint8_t *)blob;
+  const f16 *st = (const f16 *)(w + L.s_off);
+  const uint8_t *zt = has_zeros ? w + L.z_off : nullptr;
+  GemvArgs args{w, st, zt, h, nullptr, SF_F32, nullptr, bias, bias_dtype, 1, N, K, L.G,
+                has_zeros != 0, (hipStream_t)stream};
+  const SfRopeAppend rope{cos_t, sin_t, max_pos, q_out, q_dtype, k_codes, k_scales, v_codes,
+                          v_scales, scale_dtype, H, KVH, D, T_cap};
+  if (act_dtype == SF_F16) launch_pre_rope<SF_F16>(pl, args, norm_w, eps, rope, pos_dev);
+  else if (act_dtype == SF_BF16) launch_pre_rope<SF_BF16>(pl, args, norm_w, eps, rope, pos_dev);
+  else launch_pre_rope<SF_F32>(pl, args, norm_w, eps, rope, pos_dev);
+  return sf_check_launch("sf_q4_gemv_fused_rope");
 }

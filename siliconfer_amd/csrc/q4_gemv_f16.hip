@@ -5,4 +5,6 @@
 namespace sf_gemv {
 template void launch_x<SF_F16>(const GemvPlan &, const GemvArgs &);
 template void launch_pre<SF_F16>(const GemvPlan &, const GemvArgs &, int, const float *, float);
+template void launch_pre_rope<SF_F16>(const GemvPlan &, const GemvArgs &, const float *, float,
+                                      const SfRopeAppend &, const int *);
 }  // namespace sf_gemv

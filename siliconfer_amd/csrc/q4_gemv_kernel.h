@@ -318,12 +318,16 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &wq, uint32_t z, const Ac
 // clamped positions, so the norm's wave reduction runs with all lanes active.
 constexpr int PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SILU = 2;
 
-template <int B, int R, int Q, bool ASYM, int XDT, int PRE = PRE_NONE>
+// ROPE (batch 1): the workgroup's R * RS output rows are one head of the fused q|k|v projection, and instead
+// of storing them it applies RoPE and the KV-cache append to them
+// (sf_rope_append_head) at the device position *pos_dev.
+template <int B, int R, int Q, bool ASYM, int XDT, int PRE = PRE_NONE, bool ROPE = false>
 __global__ void __launch_bounds__(512)
 k_q4_gemv(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
           const uint8_t *__restrict__ ztile, const void *__restrict__ x, void *__restrict__ y,
           int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt, int N, int K,
-          int G, int cpg_shift, int C, int P, int RS, const float *__restrict__ pre_w, float eps) {
+          int G, int cpg_shift, int C, int P, int RS, const float *__restrict__ pre_w, float eps,
+          SfRopeAppend rope, const int *__restrict__ pos_dev) {
   static_assert(PRE == PRE_NONE || B == 1, "folded producers are batch-1 only");
   __shared__ float red[8][B * R];
   const int tid = threadIdx.x;
@@ -432,6 +436,31 @@ k_q4_gemv(const uint8_t *__restrict__ w, const f16 *__restrict__ stile,
   const int idx = p >> (LQ - S);
   const bool writer = (p & ((1 << (LQ - S)) - 1)) == 0;
 
+  if constexpr (ROPE) {
+    static_assert(B == 1 && Q <= 64, "the folded RoPE runs at batch 1, one wave per rowset");
+    __shared__ float hv[256];  // the head: the workgroup's R * RS rows, bias added
+    if (writer) {
+#pragma unroll
+      for (int j = 0; j < RF; ++j) {
+        const int lr = rs * R + idx * RF + j;
+        float v = acc[0][j];
+        if (bias) {
+          const int row = row0 + idx * RF + j;
+          if (bdt == SF_F32) v += ((const float *)bias)[row];
+          else if (bdt == SF_F16) v += (float)((const f16 *)bias)[row];
+          else v += sf_bf16_to_f32(((const uint16_t *)bias)[row]);
+        }
+        hv[lr] = v;
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const int pos = *pos_dev;
+      if (pos >= 0 && pos < rope.T_cap && pos < rope.max_pos)
+        sf_rope_append_head(rope, hv, blockIdx.x, pos, 0);
+    }
+    return;
+  }
   if (P <= 64) {
     if (writer) {
 #pragma unroll
@@ -504,13 +533,15 @@ inline int plan_gemv(int B, int N, int K, int g, int xdt, GemvPlan *pl, int rows
   return SF_OK;
 }
 
-template <int B, int R, int Q, bool A, int X, int PRE = PRE_NONE>
+template <int B, int R, int Q, bool A, int X, int PRE = PRE_NONE, bool ROPE = false>
 void launch_t(const GemvPlan &pl, const uint8_t *w, const f16 *st, const uint8_t *zt, const void *x,
               void *y, int ydt, float *y32, const void *bias, int bdt, int N, int K, int G,
-              hipStream_t s, const float *pre_w = nullptr, float eps = 0.f) {
-  k_q4_gemv<B, R, Q, A, X, PRE><<<pl.grid, pl.WG, 0, s>>>(w, st, zt, x, y, ydt, y32, bias, bdt, N,
-                                                          K, G, pl.cpg_shift, pl.C, pl.P, pl.RS,
-                                                          pre_w, eps);
+              hipStream_t s, const float *pre_w = nullptr, float eps = 0.f,
+              const SfRopeAppend *rope = nullptr, const int *pos_dev = nullptr) {
+  const SfRopeAppend ra = rope ? *rope : SfRopeAppend{};
+  k_q4_gemv<B, R, Q, A, X, PRE, ROPE><<<pl.grid, pl.WG, 0, s>>>(
+      w, st, zt, x, y, ydt, y32, bias, bdt, N, K, G, pl.cpg_shift, pl.C, pl.P, pl.RS, pre_w, eps, ra,
+      pos_dev);
 }
 
 template <int B, int R, int X>
@@ -585,6 +616,22 @@ void launch_pre(const GemvPlan &pl, const GemvArgs &a, int pre, const float *pre
   else SF_PRE_QA(PRE_SILU);
 #undef SF_PRE_QA
 #undef SF_PRE_T
+}
+
+// The batch-1 qkv projection with the input RMSNorm folded in and RoPE + the
+// KV-cache append folded into its epilogue; the plan has Q = 32 and R * RS
+// rows = one head per workgroup (the host checks).
+template <int X>
+void launch_pre_rope(const GemvPlan &pl, const GemvArgs &a, const float *pre_w, float eps,
+                     const SfRopeAppend &rope, const int *pos_dev) {
+  if (a.asym)
+    launch_t<1, 8, 32, true, X, PRE_RMSNORM, true>(pl, a.w, a.st, a.zt, a.x, nullptr, 0, nullptr,
+                                                   a.bias, a.bdt, a.N, a.K, a.G, a.s, pre_w, eps,
+                                                   &rope, pos_dev);
+  else
+    launch_t<1, 8, 32, false, X, PRE_RMSNORM, true>(pl, a.w, a.st, a.zt, a.x, nullptr, 0, nullptr,
+                                                    a.bias, a.bdt, a.N, a.K, a.G, a.s, pre_w, eps,
+                                                    &rope, pos_dev);
 }
 
 }  // namespace sf_gemv

@@ -249,6 +249,95 @@ __device__ __forceinline__ float sf_row_inv_rms(const float *__restrict__ x,
   return n.finish(x, delta, H, eps);
 }
 
+// RoPE + KV-cache append of one head of one row of the fused q|k|v projection
+// (rotate-half RoPE, /root/reference/siliconfer/model/layers.py:58-66, then
+// quantize_kv of kv_cache.py:49-63 into the cache), done by one whole wave:
+// x holds the head's D fp32 values (bias included), pos its position. q heads
+// go rotated to q_out row `row`; k heads rotated, v heads as they are, are
+// quantized per (head, token) — s = max|x| / 127 (1 if 0), code =
+// clip(rint(x / s)) — into the cache at pos (batch 1). Lane l owns the pairs
+// (d, d + D/2) for d = l, l + 64 (D <= 256). Shared by the RoPE/append kernel
+// and the qkv projection that folds it into its epilogue, so both store the
+// same bits.
+struct SfRopeAppend {
+  const float *cos_t, *sin_t;
+  int max_pos;
+  void *q_out;
+  int q_dtype;
+  int8_t *k_codes;
+  void *k_scales;
+  int8_t *v_codes;
+  void *v_scales;
+  int scale_dtype, H, KVH, D, T_cap;
+};
+
+__device__ __forceinline__ float sf_wave_max(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ void sf_store_dt(void *p, int dt, size_t i, float v) {
+  if (dt == SF_F32) ((float *)p)[i] = v;
+  else if (dt == SF_F16) ((f16 *)p)[i] = (f16)v;
+  else ((uint16_t *)p)[i] = sf_f32_to_bf16(v);
+}
+
+__device__ __forceinline__ void sf_rope_append_head(const SfRopeAppend &a, const float *x, int head,
+                                                    int pos, int row) {
+  const int lane = threadIdx.x & 63;
+  const int D = a.D, half = D >> 1;
+  const bool is_q = head < a.H, is_k = !is_q && head < a.H + a.KVH;
+  constexpr int MAXP = 2;  // D <= 256
+  float lo[MAXP], hi[MAXP];
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) {
+    const int d = lane + 64 * j;
+    lo[j] = hi[j] = 0.f;
+    if (d < half) {
+      const float u = x[d], w = x[d + half];
+      if (is_q || is_k) {
+        // separately rounded products, as x * cos + rotate(x) * sin in fp32
+#pragma clang fp contract(off)
+        const float c = a.cos_t[(size_t)pos * half + d], s = a.sin_t[(size_t)pos * half + d];
+        lo[j] = u * c - w * s;
+        hi[j] = w * c + u * s;
+      } else {
+        lo[j] = u;
+        hi[j] = w;
+      }
+    }
+  }
+  if (is_q) {
+#pragma unroll
+    for (int j = 0; j < MAXP; ++j) {
+      const int d = lane + 64 * j;
+      if (d < half) {
+        const size_t o = ((size_t)row * a.H + head) * D + d;
+        sf_store_dt(a.q_out, a.q_dtype, o, lo[j]);
+        sf_store_dt(a.q_out, a.q_dtype, o + half, hi[j]);
+      }
+    }
+    return;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) amax = fmaxf(amax, fmaxf(fabsf(lo[j]), fabsf(hi[j])));
+  amax = sf_wave_max(amax);
+  const float s = amax == 0.f ? 1.f : amax / 127.f;
+  const int kvh = is_k ? head - a.H : head - a.H - a.KVH;
+  const size_t crow = (size_t)kvh * a.T_cap + pos;
+  int8_t *codes = (is_k ? a.k_codes : a.v_codes) + crow * D;
+#pragma unroll
+  for (int j = 0; j < MAXP; ++j) {
+    const int d = lane + 64 * j;
+    if (d < half) {
+      codes[d] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(lo[j] / s), -128.f), 127.f);
+      codes[d + half] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(hi[j] / s), -128.f), 127.f);
+    }
+  }
+  if (lane == 0) sf_store_dt(is_k ? a.k_scales : a.v_scales, a.scale_dtype, crow, s);
+}
+
 // silu(g) * u as the decoder computes it (one formula for every kernel):
 // g * (1 / (1 + exp(-g))) * u with the hardware reciprocal (1 ulp) instead of
 // an IEEE division, which takes about ten instructions.

@@ -150,6 +150,12 @@ class LlamaModel:
         self.vlogits = torch.zeros((self.VERIFY_ROWS, self.V), dtype=f32, device=dev)
         rw = self.lib.sf_lm_head_rows_workspace_bytes(self.V, self.VERIFY_ROWS)
         self.rows_ws = torch.zeros(rw, dtype=torch.uint8, device=dev)
+        # decode: RoPE + KV append folded into the qkv projection's epilogue
+        # where its batch-1 plan gives one head per workgroup (hidden <= 1024)
+        L0 = layers[0]
+        self._qkv_rope = bool(fuse and self.lib.sf_q4_gemv_fused_rope_supported(
+            L0.qkv.out_features, L0.qkv.in_features, L0.qkv.group_size, self.Hq, self.KVH, self.D,
+            _DT[act_dtype]))
         self.pos = 0
         self.graph = None
         self._verify_graphs = {}
@@ -527,12 +533,24 @@ class LlamaModel:
                                self.h.data_ptr(), 1, self.H, self.V, st), "sf_embed")
         fuse = self.fuse
         for l, L in enumerate(self.layers):
-            if fuse:  # RMSNorm folded into the projection's activation load
-                self._gemv_fused(L.qkv, self.h, _lib.SF_PRE_RMSNORM, L.w_in, self.qkv, L.qkv_bias)
+            if self._qkv_rope:  # RMSNorm in the activation load, RoPE + append in the epilogue
+                self._chk(lib.sf_q4_gemv_fused_rope(
+                    L.qkv.blob.data_ptr(), self.h.data_ptr(), L.w_in.data_ptr(),
+                    float(self.config.rms_norm_eps), _DT[self.act_dtype],
+                    None if L.qkv_bias is None else L.qkv_bias.data_ptr(), _lib.SF_F32,
+                    self.cos.data_ptr(), self.sin.data_ptr(), self.max_seq, self.q.data_ptr(),
+                    _DT[self.q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
+                    self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, self.Hq,
+                    self.KVH, self.D, self.max_seq, pos, L.qkv.out_features, L.qkv.in_features,
+                    L.qkv.group_size, int(L.qkv.has_zeros), st), "sf_q4_gemv_fused_rope")
             else:
-                self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
-                self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
-            self._rope_append(l, self.qkv, self.q, 1, pos, 0)
+                if fuse:  # RMSNorm folded into the projection's activation load
+                    self._gemv_fused(L.qkv, self.h, _lib.SF_PRE_RMSNORM, L.w_in, self.qkv,
+                                     L.qkv_bias)
+                else:
+                    self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
+                    self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
+                self._rope_append(l, self.qkv, self.q, 1, pos, 0)
             self._chk(lib.sf_attn_decode_i8kv_dev(
                 self.q.data_ptr(), _DT[self.q.dtype], self.k_codes[l].data_ptr(),
                 self.k_scales[l].data_ptr(), self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(),

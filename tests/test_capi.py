@@ -171,3 +171,18 @@ def test_fused_rows_support_and_validation():
     assert lib.sf_q4_gemv_fused_rows(*args(9)) == -1
     assert lib.sf_q4_gemv_fused_rows(*args(2)) == -2
     assert "run sf_rmsnorm" in _lib.last_error()
+
+
+def test_fused_rope_support():
+    lib = _lib.load()
+    ok = lib.sf_q4_gemv_fused_rope_supported
+    # config 5 (hidden 896, 14/2 heads of 64): one head per workgroup of the batch-1 plan
+    for act in (_lib.SF_F16, _lib.SF_BF16, _lib.SF_F32):
+        assert ok(1152, 896, 64, 14, 2, 64, act) == 1
+    assert ok(512, 256, 64, 4, 2, 64, _lib.SF_F16) == 1
+    assert ok(6144, 4096, 128, 32, 8, 128, _lib.SF_F16) == 0   # 7B: rows per workgroup != D
+    assert ok(1000, 896, 64, 14, 2, 64, _lib.SF_F16) == 0      # N != (H + 2 KVH) D
+    rc = lib.sf_q4_gemv_fused_rope(256 * 1024, 4096, 4096, 1e-6, _lib.SF_F16, None, _lib.SF_F32,
+                                   4096, 4096, 64, 4096, _lib.SF_F16, 4096, 4096, 4096, 4096,
+                                   _lib.SF_F16, 32, 8, 128, 64, 4096, 6144, 4096, 128, 0, None)
+    assert rc == -2 and "sf_rope_kv_append instead" in _lib.last_error()

@@ -255,3 +255,50 @@ def test_residual_bias_alias_valu_and_fp32(dev, B):
         gemv_rows(lib, w, x, plain)
         torch.cuda.synchronize()
         assert torch.equal(y, plain + old), f"{xdt} B={B}"
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("H,KVH,K,asym,pos", [(14, 2, 896, False, 517), (4, 2, 256, True, 0),
+                                              (14, 2, 896, True, 63)])
+def test_qkv_rope_append_equals_separate_kernels(dev, act, H, KVH, K, asym, pos):
+    """sf_q4_gemv_fused_rope == sf_q4_gemv_fused (RMSNorm folded) then
+    sf_rope_kv_append: q_out, the cache codes and scales at *pos_dev, bit for bit."""
+    lib = _lib.load()
+    D, T_cap = 64, 64 if pos < 64 else 1024
+    N = (H + 2 * KVH) * D
+    assert lib.sf_q4_gemv_fused_rope_supported(N, K, 64, H, KVH, D, _lib._DT[act])
+    w, *_ = make_weight(dev, N, K, 64, asym, N + K + pos)
+    rng = np.random.default_rng(pos + K)
+    h = torch.as_tensor(rng.normal(0, 2, (1, K)).astype(np.float32)).to(dev)
+    nw = torch.as_tensor(rng.normal(1, 0.1, K).astype(np.float32)).to(dev)
+    bias = torch.as_tensor(rng.normal(0, 1, N).astype(np.float32)).to(dev)
+    from siliconfer_amd.model.config import ModelConfig, rope_tables
+    cfg = ModelConfig(hidden_size=K, intermediate_size=K, num_hidden_layers=1,
+                      num_attention_heads=H, num_key_value_heads=KVH, head_dim=D,
+                      vocab_size=100, rope_theta=1e6)
+    cos, sin = (torch.from_numpy(t).to(dev) for t in rope_tables(cfg, T_cap))
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=dev)
+    outs = []
+    for fold in (False, True):
+        q = torch.zeros((H, D), dtype=act, device=dev)
+        kc = torch.zeros((KVH, T_cap, D), dtype=torch.int8, device=dev)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros((KVH, T_cap), dtype=torch.float16, device=dev)
+        vs = torch.zeros_like(ks)
+        cache = (kc.data_ptr(), ks.data_ptr(), vc.data_ptr(), vs.data_ptr())
+        if fold:
+            _lib.check(lib.sf_q4_gemv_fused_rope(
+                w.blob.data_ptr(), h.data_ptr(), nw.data_ptr(), 1e-6, _lib._DT[act], bias.data_ptr(),
+                F32, cos.data_ptr(), sin.data_ptr(), T_cap, q.data_ptr(), _lib.dt(q), *cache, F16,
+                H, KVH, D, T_cap, pos_dev.data_ptr(), N, K, 64, int(asym), st()),
+                "sf_q4_gemv_fused_rope")
+        else:
+            qkv = fused(lib, w, h, _lib.SF_PRE_RMSNORM, nw, act, bias)
+            _lib.check(lib.sf_rope_kv_append(
+                qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), T_cap, q.data_ptr(), _lib.dt(q),
+                *cache, F16, 1, H, KVH, D, T_cap, pos_dev.data_ptr(), 0, st()), "sf_rope_kv_append")
+        torch.cuda.synchronize()
+        outs.append([t.cpu() for t in (q, kc, ks, vc, vs)])
+    for a, b, name in zip(*outs, ("q", "k codes", "k scales", "v codes", "v scales")):
+        assert torch.equal(a, b), name
+    assert int(outs[1][2][:, pos].count_nonzero()) == KVH   # the row at pos was written
