@@ -531,11 +531,12 @@ def profile_kernels(dev) -> None:
 def _short_kernel(name: str) -> str:
     import re
 
-    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)(?:ELi(\d))?", name)
+    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)(?:ELi(\d))?(?:ELb(\d))?", name)
     if m:
         pre = {None: "", "0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(6)]
+        rope = ",rope+append" if m.group(7) == "1" else ""
         return (f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},"
-                f"x={m.group(5)}{pre}>")
+                f"x={m.group(5)}{pre}{rope}>")
     m = re.search(r"k_q4_gemv_mfmaILi(\d+)ELb(\d)ELi(\d+)E(?:Li(\d+))?", name)
     if m:
         t = f",T={m.group(4)}" if m.group(4) else ""
