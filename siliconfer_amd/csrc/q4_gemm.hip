@@ -108,10 +108,11 @@ __device__ __forceinline__ void store_x(const XRegs<XDT> &r, uint16_t *xs_hi, ui
   }
 }
 
-// One thread's share of the W tile: 8 bytes (KPT = 16 nibbles) of row n at k,
-// and the raw scale / zero-point bits of that (row, group); converted at
-// staging (a step never straddles a group: g is a multiple of 32 and KPT
-// divides 32).
+// One thread's share of the W tile: KPT = 16 codes of row n from k (two
+// dwords of the blob's unit: k-pieces k and k + 8 of the same MFMA slice sit in
+// lanes 16 apart), and the raw scale / zero-point bits of that (row, group);
+// converted at staging (a step never straddles a group: g is a multiple of 32
+// and KPT divides 32).
 struct WRegs {
   u32x2 w;
   uint32_t sbits, zbyte;
@@ -124,7 +125,11 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *__restrict__ wq,
                                        int N, int K, int G, int g, int n, int k) {
   r.ok = n < N && k < K;
   const int nc = min(n, N - 1), kc = min(k, K - KPT);
-  r.w = *(const u32x2 *)(wq + (size_t)nc * (K >> 1) + (kc >> 1));
+  const int nb = (K + 127) >> 7, kb = kc & 127;
+  const uint8_t *unit = wq + ((size_t)(nc >> 4) * nb + (kc >> 7)) * 1024;
+  const int lane = ((kb & 31) >> 3) * 16 + (nc & 15);
+  r.w.x = *(const uint32_t *)(unit + lane * 16 + (kb >> 5) * 4);
+  r.w.y = *(const uint32_t *)(unit + (lane + 16) * 16 + (kb >> 5) * 4);
   const size_t cell = (size_t)(nc >> 3) * G + kc / g;
   r.sbits = ((const uint16_t *)st)[cell * 8 + (nc & 7)];
   if constexpr (ASYM) r.zbyte = zt[cell * 4 + ((nc & 7) >> 1)];
@@ -143,21 +148,19 @@ __device__ __forceinline__ void store_w(const WRegs &r, uint16_t *ws, uint16_t *
   if constexpr (ASYM) z = (r.zbyte >> (4 * (lrow & 1))) & 15u;
   const uint32_t keep = r.ok ? 0xFFFFFFFFu : 0u;
 #pragma unroll
-  for (int i = 0; i < KPT / 8; ++i) {  // dword i holds k = 8i .. 8i+7
+  for (int i = 0; i < KPT / 8; ++i) {  // dword i holds k = 8i .. 8i+7, code e at 4(e/2) + 16(e%2)
     const uint32_t dw = i == 0 ? r.w.x : r.w.y;
-    const uint32_t lo4 = dw & 0x0F0F0F0Fu, hi4 = (dw >> 4) & 0x0F0F0F0Fu;
     u32x4 o;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {  // pair (k = 8i + 2b, 8i + 2b + 1) = byte b of lo4 / hi4
-      // byte b of lo4 -> bits 0..7, byte b of hi4 -> bits 16..23
-      const uint32_t pq = __builtin_amdgcn_perm(hi4, lo4, 0x0c000c00u | ((4u + b) << 16) | b);
+    for (int b = 0; b < 4; ++b) {  // pair (k = 8i + 2b, 8i + 2b + 1) in the two 16-bit halves
+      const uint32_t pq = (dw >> (4 * b)) & 0x000F000Fu;
       if constexpr (MT == SF_F16) {
         // 1024 + q as fp16, minus (1024 + z): exact
         const half2_t v = sf_bitcast<half2_t>(pq | 0x64006400u) +
                           sf_bitcast<half2_t>((0xE400u | z) * 0x10001u);
         o[b] = sf_bitcast<uint32_t>(v);
       } else {
-        const float f0 = (float)(int)((pq & 0xFFu) - z), f1 = (float)(int)((pq >> 16) - z);
+        const float f0 = (float)(int)((pq & 0xFu) - z), f1 = (float)(int)((pq >> 16) - z);
         o[b] = hi_pair(sf_bitcast<uint32_t>(f0), sf_bitcast<uint32_t>(f1));
       }
     }

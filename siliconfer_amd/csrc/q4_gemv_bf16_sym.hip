@@ -1,0 +1,7 @@
+// Block-layout GEMV launches for bf16 activations, symmetric codes (one file per pair: compile time).
+#include "q4_gemv_blk.h"
+
+namespace sf_gemv {
+template void launch_blk<SF_BF16, false>(const BlkPlan &, const GemvArgs &, int, const float *, float,
+                                      const SfRopeAppend *, const int *);
+}  // namespace sf_gemv

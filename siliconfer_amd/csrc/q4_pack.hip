@@ -2,23 +2,59 @@
 //
 // The canonical form is the reference's (siliconfer/kernels/neon/__init__.py:
 // 42-81): nibble-packed rows, two's-complement (sym) or unsigned (asym) codes.
-// The blob keeps the row-major byte order — the GEMV reads it with lanes along
-// K, so consecutive lanes already load consecutive 16-byte chunks — and
-// changes three things: codes become offset-binary so one dequant path
-// serves both kinds, scales are tiled by row octets so a thread's 8 rows of
-// one group arrive in one 16-byte load, and zero-points are packed 2 per byte.
+// The blob changes four things: codes become offset-binary so one dequant path
+// serves both kinds; they are regrouped into 1 KB units of 16 rows x 128 k in
+// the order a wave's MFMA operands take them (each GEMV load instruction reads
+// one contiguous unit); scales are tiled by row octets; zero-points are packed
+// 2 per byte.
 #include "sf_common.h"
 
 namespace {
 
-__global__ void k_repack_w(const u32x4 *__restrict__ in, u32x4 *__restrict__ out, size_t n16,
-                           uint32_t xor_mask) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < n16; i += stride) {
-    u32x4 v = in[i];
-    v ^= xor_mask;
-    out[i] = v;
+// Eight canonical codes (code e at bits 4e) <-> the blob's pairing (code e at
+// bits 4 (e / 2) + 16 (e % 2)).
+__device__ __forceinline__ uint32_t pair_codes(uint32_t p) {
+  auto pack = [](uint32_t v) {  // the low nibbles of v's four bytes -> 16 bits
+    v = (v | (v >> 4)) & 0x00FF00FFu;
+    return (v | (v >> 8)) & 0x0000FFFFu;
+  };
+  return pack(p & 0x0F0F0F0Fu) | (pack((p >> 4) & 0x0F0F0F0Fu) << 16);
+}
+
+__device__ __forceinline__ uint32_t unpair_codes(uint32_t v) {
+  auto spread = [](uint32_t x) {  // 16 bits -> the low nibbles of four bytes
+    x = (x | (x << 8)) & 0x00FF00FFu;
+    return (x | (x << 4)) & 0x0F0F0F0Fu;
+  };
+  return spread(v & 0xFFFFu) | (spread(v >> 16) << 4);
+}
+
+// One thread per blob dword: unit u = o / 256, lane l = (o % 256) / 4, dword j = o % 4.
+__global__ void k_repack_w(const uint8_t *__restrict__ in, uint32_t *__restrict__ out, int N, int K,
+                           int NB, size_t ndw, uint32_t xor_mask) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < ndw; o += stride) {
+    const size_t u = o >> 8;
+    const int l = (int)((o >> 2) & 63), j = (int)(o & 3);
+    const int tile = (int)(u / NB), blk = (int)(u % NB);
+    const int row = 16 * tile + (l & 15), k0 = 128 * blk + 32 * j + 8 * (l >> 4);
+    uint32_t v = 0u;  // pad: code 8 (symmetric) / 0 after the mask
+    if (row < N && k0 < K) v = pair_codes(*(const uint32_t *)(in + (size_t)row * (K / 2) + k0 / 2));
+    out[o] = v ^ xor_mask;
+  }
+}
+
+// One thread per canonical dword (8 codes of one row).
+__global__ void k_unpack_w(const uint32_t *__restrict__ blob, uint8_t *__restrict__ out, int N, int K,
+                           int NB, uint32_t xor_mask) {
+  const size_t total = (size_t)N * (K / 8);
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
+    const int row = (int)(o / (K / 8)), k0 = 8 * (int)(o % (K / 8));
+    const int blk = k0 / 128, j = (k0 % 128) / 32, kg = (k0 % 32) / 8;
+    const size_t u = (size_t)(row / 16) * NB + blk;
+    const uint32_t v = blob[u * 256 + (size_t)(kg * 16 + row % 16) * 4 + j] ^ xor_mask;
+    *(uint32_t *)(out + (size_t)row * (K / 2) + k0 / 2) = unpair_codes(v);
   }
 }
 
@@ -100,9 +136,9 @@ extern "C" int sf_q4_repack(const uint8_t *packed, const void *scales_f16, const
   SF_REQUIRE(blob_bytes >= L.total, SF_EINVAL, "blob too small: %zu < %zu", blob_bytes, L.total);
   hipStream_t st = (hipStream_t)stream;
   uint8_t *b = (uint8_t *)blob;
-  size_t n16 = L.w_bytes / 16;
-  uint32_t mask = zeros_u8 ? 0u : 0x88888888u;
-  k_repack_w<<<grid_for(n16, 256), 256, 0, st>>>((const u32x4 *)packed, (u32x4 *)b, n16, mask);
+  const size_t ndw = L.w_bytes / 4;
+  const uint32_t mask = zeros_u8 ? 0u : 0x88888888u;
+  k_repack_w<<<grid_for(ndw, 256), 256, 0, st>>>(packed, (uint32_t *)b, N, K, L.NB, ndw, mask);
   size_t ns = (size_t)L.NT * L.G * 8;
   k_repack_s<<<grid_for(ns, 256, 0x7fffffffu), 256, 0, st>>>((const f16 *)scales_f16,
                                                              (f16 *)(b + L.s_off), N, L.G, L.NT);
@@ -126,9 +162,9 @@ extern "C" int sf_q4_unpack(const void *blob, int N, int K, int group_size, int 
   sf_blob_layout(N, K, group_size, has_zeros, &L);
   hipStream_t st = (hipStream_t)stream;
   const uint8_t *b = (const uint8_t *)blob;
-  size_t n16 = L.w_bytes / 16;
-  uint32_t mask = has_zeros ? 0u : 0x88888888u;
-  k_repack_w<<<grid_for(n16, 256), 256, 0, st>>>((const u32x4 *)b, (u32x4 *)packed, n16, mask);
+  const uint32_t mask = has_zeros ? 0u : 0x88888888u;
+  k_unpack_w<<<grid_for((size_t)N * (K / 8), 256), 256, 0, st>>>((const uint32_t *)b, packed, N, K,
+                                                                  L.NB, mask);
   size_t ns = (size_t)N * L.G;
   k_unpack_s<<<grid_for(ns, 256, 0x7fffffffu), 256, 0, st>>>((const f16 *)(b + L.s_off),
                                                              (f16 *)scales_f16, N, L.G);

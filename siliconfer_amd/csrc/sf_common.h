@@ -31,22 +31,29 @@ static inline size_t sf_align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // ---------------------------------------------------------------------------
 // int4 weight blob layout
 //
-//   [0, N*K/2)          packed nibbles in the canonical row-major order
-//                       (byte (n, j) holds k = 2j in bits 0-3 and k = 2j+1 in
-//                       bits 4-7) but OFFSET-BINARY: code + 8 for symmetric
-//                       weights (canonical byte ^ 0x88), the unsigned code for
-//                       asymmetric weights. Both kinds then dequantize as
-//                       (nibble - z) * s with z = 8 for symmetric.
+//   [0, w_bytes)        the codes, OFFSET-BINARY (code + 8 for symmetric
+//                       weights, the unsigned code for asymmetric ones; both
+//                       kinds dequantize as (code - z) * s, z = 8 when
+//                       symmetric), in 1 KB units of 16 rows x 128 k ordered
+//                       [row tile][k unit] (NTI = ceil(N/16) tiles, NB =
+//                       ceil(K/128) units per tile). Byte 16 l + 4 j + i of a
+//                       unit belongs to row 16 tile + l % 16; its dword j holds
+//                       the 8 codes of k = 128 unit + 32 j + 8 (l / 16) + e,
+//                       code e at bits 4 (e / 2) + 16 (e % 2): even codes in
+//                       the low half, odd ones in the high half, so one mask
+//                       lifts the pair (e, e + 1) into the two 16-bit lanes.
+//                       Rows past N and k past K hold code 8 (symmetric) / 0.
+//                       A wave's 64 lanes loading 16 bytes each read one unit
+//                       (1 KB contiguous) and hold the B operand of four
+//                       16x16x32 MFMAs.
 //   [s_off, ...)        fp16 scales, tiled [ceil(N/8)][G][8]: the 8 rows of a
-//                       row-octet are contiguous for each group, so a thread
-//                       that owns 8 rows of one group loads them with one
-//                       16-byte load. Pad rows hold 0.
+//                       row-octet are contiguous for each group. Pad rows hold 0.
 //   [z_off, ...)        asymmetric only: zero-points, tiled [ceil(N/8)][G][4]
 //                       bytes; byte j of a (octet, group) cell holds row 2j in
 //                       bits 0-3 and row 2j+1 in bits 4-7.
 // ---------------------------------------------------------------------------
 struct BlobLayout {
-  int N, K, g, G, NT;  // NT = row octets
+  int N, K, g, G, NT, NTI, NB;  // NT = row octets, NTI = 16-row tiles, NB = 128-k units
   size_t w_bytes, s_off, s_bytes, z_off, z_bytes, total;
 };
 
@@ -57,7 +64,9 @@ static inline bool sf_blob_layout(int N, int K, int g, int has_zeros, BlobLayout
   L->g = g;
   L->G = K / g;
   L->NT = (N + 7) / 8;
-  L->w_bytes = (size_t)N * (size_t)(K / 2);
+  L->NTI = (N + 15) / 16;
+  L->NB = (K + 127) / 128;
+  L->w_bytes = (size_t)L->NTI * L->NB * 1024;
   L->s_off = sf_align256(L->w_bytes);
   L->s_bytes = (size_t)L->NT * L->G * 8 * 2;
   L->z_off = sf_align256(L->s_off + L->s_bytes);

@@ -448,8 +448,9 @@ class LlamaModel:
         residual: up to 8 rows every projection is a batch GEMV and the o /
         down projections add into the residual rows themselves (the norms then
         read them directly). fold_*: the RMSNorm / SwiGLU before that
-        projection runs inside it (batch 1, or 3..8 rows at fp16 on the batch
-        MFMA GEMV where its plan allows) — each choice gives the same bits."""
+        projection runs inside it where the GEMV can stage the rows'
+        activations (sf_q4_gemv_fused_rows_supported) — each choice gives the
+        same bits."""
         if T not in self._rows_plans:
             L0 = self.layers[0]
             residual = T <= 8 and L0.o.in_features <= 16384 and L0.down.in_features <= 16384

@@ -50,6 +50,9 @@ def test_blob_bytes_layout():
     s_off = (w + 255) // 256 * 256
     z_off = (s_off + 608 * 14 * 16 + 255) // 256 * 256
     assert nb == z_off + 608 * 14 * 4
+    # weights come in 1 KB units of 16 rows x 128 k: 10 x 96 pads to one unit
+    assert lib.sf_q4_blob_bytes(10, 96, 32, 0) == 1024 + 2 * 3 * 16
+    assert lib.sf_q4_blob_bytes(17, 160, 32, 0) == 2 * 2 * 1024 + 3 * 5 * 16
     assert lib.sf_q4_blob_bytes(10, 100, 64, 0) == 0      # K % g != 0
     assert lib.sf_q4_blob_bytes(0, 128, 64, 0) == 0
 
@@ -153,34 +156,35 @@ def test_fused_rows_support_and_validation():
     lib = _lib.load()
     F16, F32, RMS, SILU = _lib.SF_F16, _lib.SF_F32, _lib.SF_PRE_RMSNORM, _lib.SF_PRE_SILU_MUL
     ok = lib.sf_q4_gemv_fused_rows_supported
-    # config-5 verify shapes: the two RMSNorm folds run at 3..8 rows in fp16;
-    # the down projection's plan (8 blocks per wave) keeps its SwiGLU separate;
-    # one row always folds
-    for B in (1, 3, 5, 8):
+    # config-5 verify shapes: the two RMSNorm folds run at every batch; the down
+    # projection's activations (4864 per row, two 8-k pieces per thread of a
+    # 5-wave plan) fit the LDS staging at one row only; a folded producer needs
+    # a plan of at most 8 waves
+    for B in (1, 2, 3, 5, 8):
         assert ok(RMS, B, 1152, 896, 64, 0, F16) == 1
         assert ok(RMS, B, 9728, 896, 64, 0, F16) == 1
         assert ok(SILU, B, 896, 4864, 64, 0, F16) == (B == 1)
-    assert ok(SILU, 4, 1152, 896, 64, 0, F16) == 1         # two blocks per wave: folds
-    assert ok(RMS, 2, 1152, 896, 64, 0, F16) == 0          # two rows: the VALU GEMV, unfolded
-    assert ok(RMS, 4, 1152, 896, 64, 0, F32) == 0          # fp32 activations
+    assert ok(SILU, 4, 1152, 896, 64, 0, F16) == 1
+    assert ok(RMS, 4, 1152, 896, 64, 0, F32) == 1          # fp32: high + low rows staged
     assert ok(RMS, 1, 1152, 896, 64, 0, F32) == 1
+    assert ok(RMS, 1, 4096, 16384, 128, 0, F16) == 0       # 16 waves: over the fold's 8
     assert ok(7, 4, 1152, 896, 64, 0, F16) == 0
     blob, src, y = 256 * 1024, 4096, 8192  # fake addresses: validation fails before any use
-    args = lambda B, K=896: (blob, src, RMS, src, 1e-6, F16, None, F32, y, None, F32, B, 1152, K,
-                             64, 0, None)
+    args = lambda B, op=RMS, N=1152, K=896: (blob, src, op, src, 1e-6, F16, None, F32, y, None,
+                                             F32, B, N, K, 64, 0, None)
     assert lib.sf_q4_gemv_fused_rows(*args(9)) == -1
-    assert lib.sf_q4_gemv_fused_rows(*args(2)) == -2
+    assert lib.sf_q4_gemv_fused_rows(*args(3, SILU, 896, 4864)) == -2
     assert "run sf_rmsnorm" in _lib.last_error()
 
 
 def test_fused_rope_support():
     lib = _lib.load()
     ok = lib.sf_q4_gemv_fused_rope_supported
-    # config 5 (hidden 896, 14/2 heads of 64): one head per workgroup of the batch-1 plan
+    # config 5 (hidden 896, 14/2 heads of 64): one 64-row head per workgroup
     for act in (_lib.SF_F16, _lib.SF_BF16, _lib.SF_F32):
         assert ok(1152, 896, 64, 14, 2, 64, act) == 1
     assert ok(512, 256, 64, 4, 2, 64, _lib.SF_F16) == 1
-    assert ok(6144, 4096, 128, 32, 8, 128, _lib.SF_F16) == 0   # 7B: rows per workgroup != D
+    assert ok(6144, 4096, 128, 32, 8, 128, _lib.SF_F16) == 0   # 7B: head_dim 128
     assert ok(1000, 896, 64, 14, 2, 64, _lib.SF_F16) == 0      # N != (H + 2 KVH) D
     rc = lib.sf_q4_gemv_fused_rope(256 * 1024, 4096, 4096, 1e-6, _lib.SF_F16, None, _lib.SF_F32,
                                    4096, 4096, 64, 4096, _lib.SF_F16, 4096, 4096, 4096, 4096,

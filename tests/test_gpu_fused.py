@@ -240,14 +240,15 @@ def test_fused_rows_equal_separate_kernels(dev, B, N, K, g, asym, op):
     linear.assert_close(got.cpu().numpy(), exp, 1e-3, f"fused rows op={op} B={B}")
 
 
-@pytest.mark.parametrize("B", [1, 2, 4])
-def test_residual_bias_alias_valu_and_fp32(dev, B):
-    """bias = y_f32 on the VALU GEMV (batch 1-2, and fp32 activations in
-    slices of two rows) adds each row's own previous value."""
+@pytest.mark.parametrize("B,K", [(1, 512), (2, 512), (4, 512), (4, 8192)])
+def test_residual_bias_alias(dev, B, K):
+    """bias = y_f32 adds each row's own previous value: fp16 activations, and
+    fp32 ones (staged as high and low bf16 rows; at K = 8192 four such rows
+    exceed the LDS budget and the batch runs in slices of two)."""
     lib = _lib.load()
-    w, *_ = make_weight(dev, 640, 512, 64, False, 7)
+    w, pk, s, z = make_weight(dev, 640, K, 64, False, 7)
     for xdt in (torch.float16, torch.float32):
-        x = torch.randn((B, 512), device=dev).to(xdt)
+        x = torch.randn((B, K), device=dev).to(xdt)
         old = torch.randn((B, 640), device=dev)
         y = old.clone()
         plain = torch.empty((B, 640), device=dev)
@@ -255,6 +256,9 @@ def test_residual_bias_alias_valu_and_fp32(dev, B):
         gemv_rows(lib, w, x, plain)
         torch.cuda.synchronize()
         assert torch.equal(y, plain + old), f"{xdt} B={B}"
+        exp = linear.gemv(pk, s.astype(np.float16).astype(np.float64),
+                          x.float().cpu().numpy().astype(np.float64), 64, zeros=z)
+        linear.assert_close(plain.cpu().numpy(), exp, 1e-3, f"{xdt} B={B} K={K}")
 
 
 @pytest.mark.parametrize("act", ACTS)

@@ -202,7 +202,7 @@ def test_fused_verify_equals_unfused(dev, B):
             L.w_in.mul_(1 + 0.2 * torch.randn(L.w_in.shape, generator=g, device=dev))
             L.w_post.mul_(1 + 0.2 * torch.randn(L.w_post.shape, generator=g, device=dev))
         res, fq, fg, fd = m._rows_plan(B)
-        assert res and fq == fg == (fuse and B != 2)
+        assert res and fq == fg == fuse
         rng = np.random.default_rng(48)
         m.reset()
         m.prefill(rng.integers(0, SMALL.vocab_size, 11))
