@@ -531,16 +531,16 @@ def profile_kernels(dev) -> None:
 def _short_kernel(name: str) -> str:
     import re
 
-    m = re.search(r"k_q4_gemvILi(\d)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)(?:ELi(\d))?(?:ELb(\d))?", name)
+    m = (re.search(r"k_q4_gemv_blkILi(\d)ELb(\d)ELi(\d)ELi(\d)ELi(\d+)ELb(\d)ELi(\d)ELb(\d)E", name) or
+         re.search(r"k_q4_gemv_blk<(\d), (\w+), (\d), (\d), (\d+), (\w+), (\d), (\w+)>",
+                   name.replace("true", "1").replace("false", "0")))
     if m:
-        pre = {None: "", "0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(6)]
-        rope = ",rope+append" if m.group(7) == "1" else ""
-        return (f"k_q4_gemv<B={m.group(1)},R={m.group(2)},Q={m.group(3)},asym={m.group(4)},"
-                f"x={m.group(5)}{pre}{rope}>")
-    m = re.search(r"k_q4_gemv_mfmaILi(\d+)ELb(\d)ELi(\d+)E(?:Li(\d+))?", name)
-    if m:
-        t = f",T={m.group(4)}" if m.group(4) else ""
-        return f"k_q4_gemv_mfma<LW={m.group(1)},asym={m.group(2)},BPW={m.group(3)}{t}>"
+        x = {"0": "f32", "1": "f16", "2": "bf16"}[m.group(1)]
+        pre = {"0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(7)]
+        rope = ",rope+append" if m.group(8) == "1" else ""
+        src = "lds" if m.group(6) == "1" else "direct"
+        return (f"k_q4_gemv_blk<x={x},asym={m.group(2)},gk={m.group(3)},T={m.group(4)},"
+                f"BPW={m.group(5)},{src}{pre}{rope}>")
     m = re.search(r"(k_[a-z0-9_]+|__amd_rocclr_[A-Za-z]+|at::native::[a-z_]+)", name)
     return m.group(1) if m else name[:40]
 
@@ -550,7 +550,7 @@ def sweep_launch_plan():
     once per cold copy of its blob (the count GpuSweep's cold_copies makes)."""
     plan = []
     for N, K in SHAPES:
-        blob = -(-(N * K // 2) // 256) * 256 + -(-N // 8) * (K // GROUP) * 16
+        blob = -(-N // 16) * -(-K // 128) * 1024 + -(-N // 8) * (K // GROUP) * 16
         n = max(2, -(-COLD_BYTES // blob))
         plan += [(N, K, B, n) for B in BATCHES]
     return plan
@@ -768,7 +768,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "sf_q4_gemv (k_q4_gemv at batch 1-2, k_q4_gemv_mfma at batch 4-8); average "
+            "kernel": "sf_q4_gemv (k_q4_gemv_blk: MFMA over the unit-order blob, every batch); average "
                       "over the 12 sweep cases, each timed as a graph of back-to-back cold launches "
                       "between HIP events",
             "alg_bytes_per_launch_avg": int(sum(case_bytes) / len(case_bytes)),

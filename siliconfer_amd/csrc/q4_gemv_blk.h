@@ -215,13 +215,15 @@ __device__ __forceinline__ void piece_values(const u32x4 (&q)[XPiece<XDT, PRE>::
   }
 }
 
-// Threads per workgroup a variant may run with: a folded producer holds the
-// producer's loads as well and gets the register budget of 8 waves; plain
-// variants run up to 16 waves (128 registers).
-__host__ __device__ constexpr int max_waves(int pre) { return pre != 0 ? 8 : kMaxWaves; }
+// Waves per workgroup a variant may run with: 16 (128 registers) for all but
+// the folded RMSNorm with more than four weight units per lane, which also
+// holds the norm's row loads and gets the budget of 8 waves.
+__host__ __device__ constexpr int max_waves(int pre, int t_bpw) {
+  return pre == PRE_RMSNORM && t_bpw > 4 ? 8 : kMaxWaves;
+}
 
 template <int XDT, bool ASYM, int GK, int T, int BPW, bool XL, int PRE, bool ROPE>
-__global__ void __launch_bounds__(max_waves(PRE) * 64)
+__global__ void __launch_bounds__(max_waves(PRE, T * BPW) * 64)
 k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   static_assert(XL || (PRE == PRE_NONE && XDT != SF_F32), "folded producers and fp32 activations stage in LDS");
   static_assert(!ROPE || (T == 4 && PRE == PRE_RMSNORM), "the folded RoPE takes one 64-row head per workgroup");
@@ -534,7 +536,10 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   if (wide) {
     bpw = p->nblk <= 16 ? 1 : 2;
   } else {
-    const int target = B > 4 ? 16 : 8;  // waves per workgroup
+    // waves per workgroup: 16 for larger batches, and for matrices too short
+    // to give every CU a workgroup whose K would otherwise take 8 units per
+    // wave (K is then spread over more waves)
+    const int target = B > 4 || (p->ntiles < 256 && p->nblk > 32) ? 16 : 8;
     const int need = (p->nblk + target - 1) / target;
     bpw = kBpwSet[3];
     for (int i = 0; i < 4; ++i)
@@ -543,7 +548,11 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   if (bpw > max_bpw(gk)) bpw = max_bpw(gk);
   p->BPW = bpw;
   p->nw = (p->nblk + bpw - 1) / bpw;
-  if (p->nw > max_waves(pre)) return false;
+  // the folded RMSNorm's variants hold about 16 waves per CU: two row tiles
+  // per workgroup when one would leave workgroups for a second round (T does
+  // not change any row's summation order)
+  if (pre == PRE_RMSNORM && p->T == 1 && p->BPW <= 2 && p->ntiles > 256 * (16 / p->nw)) p->T = 2;
+  if (p->nw > max_waves(pre, p->T * p->BPW)) return false;
   p->grid = (p->ntiles + p->T - 1) / p->T;
   const size_t xb = xl_bytes(B, xdt, p->nblk);
   const int per_thread = pre != PRE_NONE ? 2 : xdt == SF_F32 ? 2 : 4;
@@ -582,12 +591,15 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
 }
 
 // Runtime units-per-wave -> compiled variant. Compiled: T = 1 with every count
-// of the set the group kind allows; T = 4 (wide matrices at batch > 4, and the
-// folded RoPE) with 1, 2 and, for the RoPE, 4.
+// of the set the group kind allows; T = 2 (the folded RMSNorm on many row
+// tiles) up to 4; T = 4 (wide matrices at batch > 4, and the folded RoPE) with
+// 1, 2 and, for the RoPE, 4.
 template <int X, bool A, int GK, int T, bool XL, int PRE, bool ROPE>
 void by_bpw(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
             const SfRopeAppend *rope, const int *pos_dev) {
-  constexpr int MB = T == 4 ? (GK == 2 ? (ROPE ? 2 : 0) : ROPE ? 4 : 2) : GK == 2 ? 4 : 8;
+  constexpr int MB = T == 4   ? (GK == 2 ? (ROPE ? 2 : 0) : ROPE ? 4 : 2)
+                     : T == 2 ? (GK == 2 ? 2 : 4)
+                              : GK == 2 ? 4 : 8;
 #define SF_BPW(N)                                                                 \
   case N:                                                                         \
     if constexpr (N <= MB) launch_cfg<X, A, GK, T, N, XL, PRE, ROPE>(p, g, pre_w, eps, rope, pos_dev); \
@@ -611,7 +623,8 @@ void by_mode(const BlkPlan &p, const GemvArgs &g, int pre, const float *pre_w, f
     if (p.T == 4) by_bpw<X, A, GK, 4, XL, PRE, false>(p, g, pre_w, eps, rope, pos_dev); \
     else by_bpw<X, A, GK, 1, XL, PRE, false>(p, g, pre_w, eps, rope, pos_dev);         \
   } while (0)
-  if (pre == PRE_RMSNORM) SF_T(true, PRE_RMSNORM);
+  if (pre == PRE_RMSNORM && p.T == 2) by_bpw<X, A, GK, 2, true, PRE_RMSNORM, false>(p, g, pre_w, eps, rope, pos_dev);
+  else if (pre == PRE_RMSNORM) SF_T(true, PRE_RMSNORM);
   else if (pre == PRE_SILU) SF_T(true, PRE_SILU);
   else if (p.xl) SF_T(true, PRE_NONE);
   else if constexpr (X != SF_F32) SF_T(false, PRE_NONE);

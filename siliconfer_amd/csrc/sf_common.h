@@ -225,19 +225,23 @@ struct SfRowNorm {
       };
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc(v[u], lane + 64 * u < n4);
+      // the rest in batches of 4 float4 per lane, in the same order as one
+      // batch of 8 (so the sum is the same bits; fewer registers held)
       for (int base = 0; base < n4; base += 512) {
-        const int u0 = base == 0 ? 4 : 0;  // the first pass's u < 4 came from issue()
-        if (base + 64 * u0 >= n4) break;   // nothing left in range (adds only zeros)
-        float4_t w[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = min(base + lane + 64 * u, n4 - 1);
-          w[u] = x4[i];
-          if (delta) w[u] += d4[i];
+        for (int h = 0; h < 2; ++h) {
+          if (base == 0 && h == 0) continue;  // the first pass's u < 4 came from issue()
+          if (base + 256 * h >= n4) break;    // nothing left in range (adds only zeros)
+          float4_t w[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int i = min(base + 256 * h + lane + 64 * u, n4 - 1);
+            w[u] = x4[i];
+            if (delta) w[u] += d4[i];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc(w[u], base + 256 * h + lane + 64 * u < n4);
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (u >= u0) acc(w[u], base + lane + 64 * u < n4);
       }
     } else {
       for (int h = lane; h < H; h += 64) {

@@ -158,16 +158,16 @@ def test_fused_rows_support_and_validation():
     ok = lib.sf_q4_gemv_fused_rows_supported
     # config-5 verify shapes: the two RMSNorm folds run at every batch; the down
     # projection's activations (4864 per row, two 8-k pieces per thread of a
-    # 5-wave plan) fit the LDS staging at one row only; a folded producer needs
-    # a plan of at most 8 waves
+    # 10-wave plan) fit the LDS staging up to two rows; the folded RMSNorm
+    # needs a plan of at most 8 waves
     for B in (1, 2, 3, 5, 8):
         assert ok(RMS, B, 1152, 896, 64, 0, F16) == 1
         assert ok(RMS, B, 9728, 896, 64, 0, F16) == 1
-        assert ok(SILU, B, 896, 4864, 64, 0, F16) == (B == 1)
+        assert ok(SILU, B, 896, 4864, 64, 0, F16) == (B <= 2)
     assert ok(SILU, 4, 1152, 896, 64, 0, F16) == 1
     assert ok(RMS, 4, 1152, 896, 64, 0, F32) == 1          # fp32: high + low rows staged
     assert ok(RMS, 1, 1152, 896, 64, 0, F32) == 1
-    assert ok(RMS, 1, 4096, 16384, 128, 0, F16) == 0       # 16 waves: over the fold's 8
+    assert ok(RMS, 1, 4096, 16384, 128, 0, F16) == 0       # 16 waves of 8 units: over the cap
     assert ok(7, 4, 1152, 896, 64, 0, F16) == 0
     blob, src, y = 256 * 1024, 4096, 8192  # fake addresses: validation fails before any use
     args = lambda B, op=RMS, N=1152, K=896: (blob, src, op, src, 1e-6, F16, None, F32, y, None,
