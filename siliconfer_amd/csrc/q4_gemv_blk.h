@@ -504,7 +504,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 // ---------------------------------------------------------------------------
 // Units per wave come from a compiled set so that every register array has a
 // compile-time size and every load can be issued before the first MFMA.
-constexpr int kBpwSet[4] = {1, 2, 4, 8};
+constexpr int kBpwSet[5] = {1, 2, 4, 8, 12};
 
 struct BlkPlan {
   int T, BPW, nw, grid, nblk, ntiles, xl, xp;
@@ -514,8 +514,10 @@ struct BlkPlan {
 inline int group_kind(int g) { return g % 128 == 0 ? 0 : g == 64 ? 1 : 2; }
 
 // The most units per wave a group kind's registers allow (scale and zero bits
-// per unit grow with the slots).
-inline int max_bpw(int gk) { return gk == 2 ? 4 : 8; }
+// per unit grow with the slots; the bf16 path holds the slots' sums as well).
+__host__ __device__ constexpr int max_bpw(int gk, bool bf) {
+  return gk == 0 ? (bf ? 8 : 12) : gk == 1 ? (bf ? 4 : 8) : 4;
+}
 
 inline size_t xl_bytes(int B, int xdt, int nblk) {
   const int rows = xdt == SF_F32 ? 2 * B : B;
@@ -536,16 +538,16 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   if (wide) {
     bpw = p->nblk <= 16 ? 1 : 2;
   } else {
-    // waves per workgroup: 16 for larger batches, and for matrices too short
-    // to give every CU a workgroup whose K would otherwise take 8 units per
-    // wave (K is then spread over more waves)
-    const int target = B > 4 || (p->ntiles < 256 && p->nblk > 32) ? 16 : 8;
+    // waves per workgroup: 16 for larger batches, and for matrices with at
+    // most one workgroup per CU and a K of at least 32 units (K is then
+    // spread over more waves)
+    const int target = B > 4 || (p->ntiles <= 256 && p->nblk >= 32) ? 16 : 8;
     const int need = (p->nblk + target - 1) / target;
-    bpw = kBpwSet[3];
-    for (int i = 0; i < 4; ++i)
+    bpw = kBpwSet[4];
+    for (int i = 0; i < 5; ++i)
       if (kBpwSet[i] >= need) { bpw = kBpwSet[i]; break; }
   }
-  if (bpw > max_bpw(gk)) bpw = max_bpw(gk);
+  if (bpw > max_bpw(gk, xdt != SF_F16)) bpw = max_bpw(gk, xdt != SF_F16);
   p->BPW = bpw;
   p->nw = (p->nblk + bpw - 1) / bpw;
   // the folded RMSNorm's variants hold about 16 waves per CU: two row tiles
@@ -599,13 +601,13 @@ void by_bpw(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
             const SfRopeAppend *rope, const int *pos_dev) {
   constexpr int MB = T == 4   ? (GK == 2 ? (ROPE ? 2 : 0) : ROPE ? 4 : 2)
                      : T == 2 ? (GK == 2 ? 2 : 4)
-                              : GK == 2 ? 4 : 8;
+                              : max_bpw(GK, X != SF_F16);
 #define SF_BPW(N)                                                                 \
   case N:                                                                         \
     if constexpr (N <= MB) launch_cfg<X, A, GK, T, N, XL, PRE, ROPE>(p, g, pre_w, eps, rope, pos_dev); \
     break;
   switch (p.BPW) {
-    SF_BPW(1) SF_BPW(2) SF_BPW(4) SF_BPW(8)
+    SF_BPW(1) SF_BPW(2) SF_BPW(4) SF_BPW(8) SF_BPW(12)
     default: break;
   }
 #undef SF_BPW
