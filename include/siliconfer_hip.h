@@ -76,12 +76,12 @@ int sf_q4_unpack(const void *blob, int N, int K, int group_size, int has_zeros,
  * y[b, n] = sum_g s[n,g] * sum_{k in g} (q[n,k] - z[n,g]) x[b,k]   (z = 0 sym)
  * Replaces q4_gemv_sym / q4_gemv_asym (bindings.cpp:45-93) and, through
  * Q4Linear at T<=8 rows, q4_gemm_sym / q4_gemm_asym (bindings.cpp:98-150).
- * x: [B, K] of x_dtype (SF_F16 or SF_BF16). Outputs: y [B, N] of y_dtype
+ * x: [B, K] of x_dtype (SF_F16, SF_BF16 or SF_F32). Outputs: y [B, N] of y_dtype
  * (SF_F16 / SF_BF16 / SF_F32), and/or y_f32 [B, N]; either may be NULL but
  * not both. bias: NULL, [N] of bias_dtype (added before the store), or y_f32
  * itself (fp32: each output adds its own previous value, per batch row — a
- * residual add). fp32
- * accumulation throughout. */
+ * residual add). fp32 accumulation throughout. K up to 16384 (8192 for group
+ * sizes that are not a multiple of 64), else SF_EUNSUPPORTED. */
 int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
                const void *bias, int bias_dtype, int B, int N, int K, int group_size,
                int has_zeros, void *stream);
@@ -106,12 +106,13 @@ int sf_q4_gemv_fused(const void *blob, const float *src, int op, const float *no
 /* sf_q4_gemv_fused over B = 1..8 rows (src [B][K], or [B][2K] gate|up): the
  * target's verify rows of speculative decoding (engine/speculative.py:280)
  * with each RMSNorm / SwiGLU folded into the next projection as the decode
- * step does. B = 1 is sf_q4_gemv_fused; B = 3..8 with fp16 activations runs
- * the batch MFMA GEMV with the producer folded into its activation load, and
- * equals sf_rmsnorm / sf_silu_mul followed by sf_q4_gemv bit for bit. Other
- * shapes return SF_EUNSUPPORTED; sf_q4_gemv_fused_rows_supported says which
- * (1 = supported). bias may be y_f32 itself (each row adds its own previous
- * value), as for sf_q4_gemv. */
+ * step does. B = 1 is sf_q4_gemv_fused. The producer runs while the GEMV
+ * stages its activations, and the result equals sf_rmsnorm / sf_silu_mul
+ * followed by sf_q4_gemv bit for bit. Shapes whose B rows of activations do
+ * not fit the staging (or whose RMSNorm plan exceeds its wave budget) return
+ * SF_EUNSUPPORTED; sf_q4_gemv_fused_rows_supported says which (1 = supported).
+ * bias may be y_f32 itself (each row adds its own previous value), as for
+ * sf_q4_gemv. */
 int sf_q4_gemv_fused_rows_supported(int op, int B, int N, int K, int group_size, int has_zeros,
                                     int act_dtype);
 int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op, const float *norm_w,
@@ -123,8 +124,9 @@ int sf_q4_gemv_fused_rows(const void *blob, const float *src, int op, const floa
  * activation load (sf_q4_gemv_fused, SF_PRE_RMSNORM) and RoPE + the KV-cache
  * append (sf_rope_kv_append at the device position *pos_dev) folded into its
  * epilogue: q_out [H][D] and the cache row at *pos_dev get the same bits as
- * those two calls; the fp32 q|k|v rows are not stored. Needs one head per
- * workgroup of the batch-1 plan (in_features <= 1024 for D = 64);
+ * those two calls; the fp32 q|k|v rows are not stored. Needs D = 64 (one
+ * 64-row head per workgroup) and a batch-1 plan of at most four weight units
+ * per wave (in_features <= 4096 for groups of 64 / 128);
  * sf_q4_gemv_fused_rope_supported says so (1), else SF_EUNSUPPORTED. No
  * counterpart in the reference (layers.py:93-112 runs these as separate ops). */
 int sf_q4_gemv_fused_rope_supported(int N, int K, int group_size, int H, int KVH, int D,

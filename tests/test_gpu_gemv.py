@@ -187,14 +187,18 @@ def test_repeated_launches_bitwise_identical(dev):
 
 
 @pytest.mark.parametrize("asym", [False, True])
-def test_repack_round_trip_bit_exact(dev, asym):
+@pytest.mark.parametrize("N,K,g", [(37, 384, 128), (21, 96, 32), (16, 160, 32), (50, 640, 64)])
+def test_repack_round_trip_bit_exact(dev, asym, N, K, g):
+    """canonical -> unit-order blob -> canonical, bit for bit; N not a multiple
+    of the 16-row tile and K not a multiple of the 128-k unit exercise the
+    padding."""
     rng = np.random.default_rng(5)
-    W = rng.normal(0, 1, (37, 384)).astype(np.float32)
+    W = rng.normal(0, 1, (N, K)).astype(np.float32)
     if asym:
-        pk, s, z = P.pack_weights_asym(W, 128)
+        pk, s, z = P.pack_weights_asym(W, g)
     else:
-        (pk, s), z = P.pack_weights_sym(W, 128), None
-    w = Q4Weight(pk, s, z, 128, device=dev)
+        (pk, s), z = P.pack_weights_sym(W, g), None
+    w = Q4Weight(pk, s, z, g, device=dev)
     pk2, s2, z2 = w.canonical()
     np.testing.assert_array_equal(pk2.cpu().numpy(), pk)
     np.testing.assert_array_equal(s2.cpu().numpy(), s.astype(np.float16))
@@ -224,17 +228,18 @@ def test_unit_vector_activations_pin_row_and_k_mapping(dev, xdtype, N, K, g):
 
 
 @pytest.mark.parametrize("N,K,g,asym", [
-    (13, 64, 64, False),       # one 64-k block, rows far below a 16-row tile
-    (1000, 896, 64, True),     # 14 blocks over 7 waves, ragged last tile
-    (77, 4864, 64, False),     # 76 blocks: 7 waves of 12 (the last one shorter)
-    (4100, 11008, 128, True),  # 86 blocks of 128 k: 8 waves of 12, the last of 2
-    (64, 12288, 128, False),   # largest K on 16-byte lanes (8 waves x 12 blocks)
-    (48, 12288, 64, True),     # largest K on 8-byte lanes (8 waves x 24 blocks)
-    (40, 2048, 256, False),    # groups of 256 take the VALU kernel
+    (13, 64, 64, False),       # half a 128-k unit, rows far below a 16-row tile
+    (1000, 896, 64, True),     # 7 units over 7 waves, ragged last tile
+    (77, 4864, 64, False),     # 38 units: 10 waves of 4 (the last of 2)
+    (4100, 11008, 128, True),  # 86 units, wide: four row tiles per workgroup at batch > 4
+    (64, 12288, 128, False),   # 96 units: 16 waves of 8 at batch > 4
+    (48, 12288, 64, True),     # 96 units at g = 64: two scale groups per unit
+    (40, 2048, 256, False),    # groups of 256: one group over two units
 ])
 def test_batch3to8_shapes(dev, N, K, g, asym):
-    """Batch 3..8 with fp16 activations and groups of 64 or 128 run on MFMA:
-    ragged row tiles, uneven K splits over waves, both load widths."""
+    """Batch 3..8 with fp16 activations: ragged row tiles, uneven K splits over
+    waves, LDS-staged (batch <= 4) and directly loaded (batch > 4)
+    activations, groups spanning half, one and two units."""
     rng = np.random.default_rng(N + K)
     W = rng.normal(0.01 if asym else 0, 0.02, (N, K)).astype(np.float32)
     if asym:
