@@ -120,6 +120,7 @@ struct BlkArgs {
   int bdt;
   int B, N, K, G, g, nblk, ntiles;
   uint32_t gmul;      // ceil(2^30 / g): k / g = (k * gmul) >> 30
+  int uq, ur;         // units per wave: uq, one more for the first ur waves
   int xp;             // LDS row pitch of the staged activations (elements)
   const float *pre_w; // RMSNorm weight (PRE_RMSNORM)
   float eps;
@@ -249,8 +250,10 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     nt[t] = min(n0 + t * 16 + nl, a.N - 1);  // rows past N: a valid row's scales, never stored
     ti[t] = min((int)blockIdx.x * T + t, a.ntiles - 1);
   }
-  const int blk0 = wave * BPW;  // the host launches only waves with blk0 < nblk
-  const int cnt = min(BPW, a.nblk - blk0);
+  // K split: wave w takes uq units, one more for the first ur waves, and the
+  // last wave what is left (1 <= cnt <= BPW)
+  const int blk0 = wave * a.uq + min(wave, a.ur);
+  const int cnt = min(a.uq + (wave < a.ur ? 1 : 0), a.nblk - blk0);
   const int blast = blk0 + cnt - 1;  // units past the wave's own re-read its last one
 
   uint16_t *const xl = (uint16_t *)smem;                               // XL: [rows][xp]
@@ -401,6 +404,9 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   for (int i = 0; i < BPW; ++i) {
     if constexpr (!XL)
       if (i + XPRE < BPW) xload(i + XPRE);
+    // XL: units past the wave's share are skipped (a wave-uniform branch
+    // around straight-line code: every register array keeps a fixed index)
+    if (XL && i >= cnt) continue;
     const int kb = min(blk0 + i, blast) * kUnitK;
     u32x4 av[4];
 #pragma unroll
@@ -447,10 +453,12 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
         uint32_t sb = sbits[t][i][sl];
         asm volatile("" : "+v"(sb));  // convert at the point of use (keeps the load in flight)
         const float s = (float)sf_bitcast<f16>((uint16_t)sb);
-        // units past the wave's own (last wave only) are dropped here: a branch
-        // instead would let the compiler sink their loads into it
+        // units past the wave's own: skipped by the branch around the unit
+        // (XL), or computed and dropped here (direct: a branch would let the
+        // compiler sink their loads into it; in XL mode the barrier after the
+        // staging keeps every load above it)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = i < cnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
+        for (int r = 0; r < 4; ++r) acc[t][r] = XL || i < cnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
       }
     }
   }
@@ -507,7 +515,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 constexpr int kBpwSet[5] = {1, 2, 4, 8, 12};
 
 struct BlkPlan {
-  int T, BPW, nw, grid, nblk, ntiles, xl, xp;
+  int T, BPW, nw, grid, nblk, ntiles, xl, xp, uq, ur;
   size_t lds;
 };
 
@@ -534,7 +542,14 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   const int gk = group_kind(g);
   const bool wide = B > 4 && p->ntiles >= 512 && p->nblk <= 32 && gk != 2;
   p->T = rope ? 4 : wide ? 4 : 1;
-  int bpw;
+  const int maxb = max_bpw(gk, xdt != SF_F16);
+  const size_t xb = xl_bytes(B, xdt, p->nblk);
+  auto bucket = [](int need) {
+    for (int i = 0; i < 5; ++i)
+      if (kBpwSet[i] >= need) return kBpwSet[i];
+    return kBpwSet[4];
+  };
+  int bpw, nw;
   if (wide) {
     bpw = p->nblk <= 16 ? 1 : 2;
   } else {
@@ -542,21 +557,20 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
     // most one workgroup per CU and a K of at least 32 units (K is then
     // spread over more waves)
     const int target = B > 4 || (p->ntiles <= 256 && p->nblk >= 32) ? 16 : 8;
-    const int need = (p->nblk + target - 1) / target;
-    bpw = kBpwSet[4];
-    for (int i = 0; i < 5; ++i)
-      if (kBpwSet[i] >= need) { bpw = kBpwSet[i]; break; }
+    bpw = bucket((p->nblk + target - 1) / target);
   }
-  if (bpw > max_bpw(gk, xdt != SF_F16)) bpw = max_bpw(gk, xdt != SF_F16);
+  if (bpw > maxb) bpw = maxb;
+  nw = (p->nblk + bpw - 1) / bpw;
   p->BPW = bpw;
-  p->nw = (p->nblk + bpw - 1) / bpw;
+  p->nw = nw;
+  p->uq = bpw;  // units per wave; the last wave takes what is left
+  p->ur = 0;
   // the folded RMSNorm's variants hold about 16 waves per CU: two row tiles
   // per workgroup when one would leave workgroups for a second round (T does
   // not change any row's summation order)
   if (pre == PRE_RMSNORM && p->T == 1 && p->BPW <= 2 && p->ntiles > 256 * (16 / p->nw)) p->T = 2;
   if (p->nw > max_waves(pre, p->T * p->BPW)) return false;
   p->grid = (p->ntiles + p->T - 1) / p->T;
-  const size_t xb = xl_bytes(B, xdt, p->nblk);
   const int per_thread = pre != PRE_NONE ? 2 : xdt == SF_F32 ? 2 : 4;
   const bool xl_fit = xb <= (size_t)kXlMaxBytes &&
                       (size_t)B * (K / 8) <= (size_t)per_thread * p->nw * 64;
@@ -587,7 +601,7 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
   }
   const uint32_t gmul = (uint32_t)(((1ull << 30) + g.g - 1) / g.g);
   const BlkArgs ba{g.w, g.st, g.zt, g.x, g.y, g.ydt, g.y32, g.bias, g.bdt, g.B, g.N, g.K, g.G, g.g,
-                   p.nblk, p.ntiles, gmul, p.xp, pre_w, eps};
+                   p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps};
   const SfRopeAppend ra = rope ? *rope : SfRopeAppend{};
   k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE><<<p.grid, p.nw * 64, p.lds, g.s>>>(ba, ra, pos_dev);
 }
