@@ -404,9 +404,6 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   for (int i = 0; i < BPW; ++i) {
     if constexpr (!XL)
       if (i + XPRE < BPW) xload(i + XPRE);
-    // XL: units past the wave's share are skipped (a wave-uniform branch
-    // around straight-line code: every register array keeps a fixed index)
-    if (XL && i >= cnt) continue;
     const int kb = min(blk0 + i, blast) * kUnitK;
     u32x4 av[4];
 #pragma unroll
@@ -453,12 +450,12 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
         uint32_t sb = sbits[t][i][sl];
         asm volatile("" : "+v"(sb));  // convert at the point of use (keeps the load in flight)
         const float s = (float)sf_bitcast<f16>((uint16_t)sb);
-        // units past the wave's own: skipped by the branch around the unit
-        // (XL), or computed and dropped here (direct: a branch would let the
-        // compiler sink their loads into it; in XL mode the barrier after the
-        // staging keeps every load above it)
+        // units past the wave's own (last wave only) are computed on re-read
+        // data and dropped here: a branch around them would cut the unrolled
+        // units into blocks the scheduler cannot interleave (and, without the
+        // staging barrier, let the compiler sink their loads into it)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = XL || i < cnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
+        for (int r = 0; r < 4; ++r) acc[t][r] = i < cnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
       }
     }
   }
@@ -512,7 +509,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 // ---------------------------------------------------------------------------
 // Units per wave come from a compiled set so that every register array has a
 // compile-time size and every load can be issued before the first MFMA.
-constexpr int kBpwSet[5] = {1, 2, 4, 8, 12};
+constexpr int kBpwSet[6] = {1, 2, 4, 8, 11, 12};  // 11: K = 11008 (86 units) over 8 waves
 
 struct BlkPlan {
   int T, BPW, nw, grid, nblk, ntiles, xl, xp, uq, ur;
@@ -545,9 +542,9 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   const int maxb = max_bpw(gk, xdt != SF_F16);
   const size_t xb = xl_bytes(B, xdt, p->nblk);
   auto bucket = [](int need) {
-    for (int i = 0; i < 5; ++i)
+    for (int i = 0; i < 6; ++i)
       if (kBpwSet[i] >= need) return kBpwSet[i];
-    return kBpwSet[4];
+    return kBpwSet[5];
   };
   int bpw, nw;
   if (wide) {
@@ -555,7 +552,7 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   } else {
     // waves per workgroup: 16 for larger batches, and for matrices with at
     // most one workgroup per CU and a K of at least 32 units (K is then
-    // spread over more waves)
+    // spread over more waves; measured on 4096 x 4096 and 4096 x 11008)
     const int target = B > 4 || (p->ntiles <= 256 && p->nblk >= 32) ? 16 : 8;
     bpw = bucket((p->nblk + target - 1) / target);
   }
@@ -621,7 +618,7 @@ void by_bpw(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
     if constexpr (N <= MB) launch_cfg<X, A, GK, T, N, XL, PRE, ROPE>(p, g, pre_w, eps, rope, pos_dev); \
     break;
   switch (p.BPW) {
-    SF_BPW(1) SF_BPW(2) SF_BPW(4) SF_BPW(8) SF_BPW(12)
+    SF_BPW(1) SF_BPW(2) SF_BPW(4) SF_BPW(8) SF_BPW(11) SF_BPW(12)
     default: break;
   }
 #undef SF_BPW
