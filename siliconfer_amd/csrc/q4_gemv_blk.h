@@ -520,9 +520,13 @@ inline int group_kind(int g) { return g % 128 == 0 ? 0 : g == 64 ? 1 : 2; }
 
 // The most units per wave a group kind's registers allow (scale and zero bits
 // per unit grow with the slots; the bf16 path holds the slots' sums as well).
+// With 16 waves this covers K up to 16384 for groups of 64 and 128 (8192 for
+// other multiples of 32). The bf16 path at groups of 64 keeps to 4 units where
+// 16 waves suffice: its 8-unit variants spill registers (correct, slower).
 __host__ __device__ constexpr int max_bpw(int gk, bool bf) {
-  return gk == 0 ? (bf ? 8 : 12) : gk == 1 ? (bf ? 4 : 8) : 4;
+  return gk == 0 ? (bf ? 8 : 12) : gk == 1 ? 8 : 4;
 }
+inline int soft_max_bpw(int gk, bool bf) { return gk == 1 && bf ? 4 : max_bpw(gk, bf); }
 
 inline size_t xl_bytes(int B, int xdt, int nblk) {
   const int rows = xdt == SF_F32 ? 2 * B : B;
@@ -556,7 +560,8 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
     const int target = B > 4 || (p->ntiles <= 256 && p->nblk >= 32) ? 16 : 8;
     bpw = bucket((p->nblk + target - 1) / target);
   }
-  if (bpw > maxb) bpw = maxb;
+  const int soft = soft_max_bpw(gk, xdt != SF_F16);
+  if (bpw > soft) bpw = (p->nblk + soft - 1) / soft <= kMaxWaves ? soft : maxb;
   nw = (p->nblk + bpw - 1) / bpw;
   p->BPW = bpw;
   p->nw = nw;

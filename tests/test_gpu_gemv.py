@@ -135,6 +135,32 @@ def test_bf16_and_f32_activations(dev, xdtype, asym):
         linear.assert_close(y32, ref, TOL, f"{xdtype} asym={asym} B={B}")
 
 
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N,K,g,asym", [
+    (130, 160, 32, True),      # K past the last whole unit; a scale group per MFMA
+    (64, 1344, 96, False),     # groups of 96 (not a power of two), half a unit at the end
+    (4100, 4096, 64, True),    # wide: four row tiles per workgroup at batch > 4
+    (48, 12288, 64, True),     # 96 units, two scale groups per unit, zero-points
+    (300, 8192, 128, False),   # fp32: four rows' high and low parts exceed the LDS budget
+])
+def test_activation_dtypes_and_batches(dev, xdtype, N, K, g, asym):
+    """Every activation dtype at batch 1..8 over the GEMV's paths: LDS-staged
+    and directly loaded activations, fp32 rows in batch slices, group sizes
+    that fold per unit, per two MFMAs and per MFMA, K not a multiple of the
+    128-k unit. Against the oracle on the activations as the kernel saw them."""
+    rng = np.random.default_rng(N * 7 + K)
+    W = rng.normal(0.01 if asym else 0, 0.02, (N, K)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, g)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, g), None
+    x = rng.normal(0, 2, (8, K)).astype(np.float32)
+    for B in (1, 3, 6, 8):
+        y32, _, xk = run_gemv(dev, pk, s, z, x[:B], g, xdtype=xdtype)
+        ref = linear.gemv(pk, s16(s), xk.astype(np.float64), g, zeros=z)
+        linear.assert_close(y32, ref, TOL, f"{xdtype} N={N} K={K} g={g} asym={asym} B={B}")
+
+
 @pytest.mark.parametrize("N,K,g", [
     (1, 128, 128),      # single row (test_kernel.py:121-129)
     (13, 128, 64),      # rows not a multiple of 8; 4 lanes per row
