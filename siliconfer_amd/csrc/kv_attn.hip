@@ -594,10 +594,10 @@ constexpr int attn_mfma_smem_floats() {
 }
 
 // NW waves per workgroup, NB of a wave's tiles in flight. NW = 4 serves
-// split-T launches (the cross-split merge runs on 256 threads); NW = 8 serves
-// one split per (b, kv head): with 4 tiles per wave in flight (2 at head_dim
-// 128, for registers), a 1024-token cache is one round of loads and needs no
-// cross-workgroup merge.
+// split-T launches (the cross-split merge runs on 256 threads); one split per
+// (b, kv head) runs 16 waves with one tile each in flight at head_dim 64 (more
+// tiles per wave spill at 128 VGPRs) and 8 waves with 2 at head_dim 128, so a
+// 512-token cache is one round of loads and needs no cross-workgroup merge.
 // Splits start on 32-token boundaries (tile rounded up to a multiple of 32), so
 // when T_cap % 4 == 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
 template <int QDT, int SDT, int D, int NW, int NB>
@@ -608,7 +608,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
             int T, const int *__restrict__ T_dev, int causal, int T_cap, float qscale,
             int n_splits, int vscale) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  static_assert(NW == kAttnWaves || NW == 8, "4 waves (split-T) or 8 (one split)");
+  static_assert(NW == kAttnWaves || NW == 8 || NW == 16, "4 waves (split-T), 8 or 16 (one split)");
   constexpr int NT = NW * 64;
   constexpr int KS = D / 32;       // q.k k-steps per token
   constexpr int DB = D / 16;       // P V dim blocks
@@ -1002,7 +1002,7 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
 #define SF_MFMA_D(QD, SD)                                   \
   do {                                                      \
     if (n_splits == 1) {                                    \
-      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, 8, 4);        \
+      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, 16, 1);       \
       else SF_MFMA_LAUNCH(QD, SD, 128, 8, 2);               \
     } else {                                                \
       if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, kAttnWaves, 2); \
