@@ -203,3 +203,14 @@ def test_sixteen_heads_d128(dev, T, S):
     shorter than a tile, and many splits."""
     rng = np.random.default_rng(40 + T)
     check(dev, *make_inputs(rng, 1, 32, 2, 128, T), n_tiles=S, what=f"G=16 D=128 T={T} S={S}")
+
+
+@pytest.mark.parametrize("T", [480, 512, 513, 545, 1024])
+def test_one_split_wave_rounds(dev, T):
+    """One split at head_dim 64 runs 16 waves, one 32-token tile each per round:
+    15, 16 and 17 tiles (one wave takes a second tile), a partial last tile, and
+    two full rounds."""
+    rng = np.random.default_rng(50 + T)
+    check(dev, *make_inputs(rng, 1, 14, 2, 64, T), n_tiles=1, what=f"one split T={T}")
+    check(dev, *make_inputs(rng, 2, 14, 2, 64, T, np.float16), n_tiles=1,
+          what=f"one split B=2 fp16 scales T={T}")
