@@ -176,7 +176,12 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
  * calls of any shape. Calls that share a workspace must not overlap (use one
  * workspace per stream). */
 size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
+/* Default split count (the reference's _choose_n_tiles, q4_attention.py:183-197,
+ * re-tuned for MI355X): one split up to 1280 cached tokens at head_dim <= 64
+ * and up to 640 above, then about 128 tokens per split, at most 64.
+ * sf_attn_default_splits is the head_dim-64 rule. */
 int sf_attn_default_splits(int B, int KVH, int T);
+int sf_attn_default_splits_d(int B, int KVH, int T, int D);
 int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const void *k_scales,
                         const int8_t *v_codes, const void *v_scales, int scale_dtype, void *out,
                         int out_dtype, void *workspace, size_t workspace_bytes, int B, int H,
@@ -185,7 +190,7 @@ int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const
 
 /* The same attention with its length in device memory: T = *T_dev + T_add
  * (for decode steps replayed from a HIP graph, where the length grows by one
- * token per replay). n_splits (<= 0: sf_attn_default_splits at T_max) and the
+ * token per replay). n_splits (<= 0: sf_attn_default_splits_d at T_max) and the
  * workspace are fixed for T <= T_max. Same reference interface as above. */
 int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
                             const void *k_scales, const int8_t *v_codes, const void *v_scales,
@@ -207,7 +212,7 @@ int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes, cons
 /* The same causal attention with T0 in device memory (*T0_dev, read when the
  * kernel runs): the verify rows of speculative decoding replayed from a HIP
  * graph at a position the host does not know when it records the launch.
- * n_splits (<= 0: sf_attn_default_splits(T_q, KVH, T_max)) and the workspace
+ * n_splits (<= 0: sf_attn_default_splits_d(T_q, KVH, T_max, D)) and the workspace
  * (sf_attn_workspace_bytes(T_q, H, D, n_splits), zero-filled before its first
  * use) are fixed for T0 + T_q <= T_max; rows past T_cap see T_cap tokens. */
 int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,

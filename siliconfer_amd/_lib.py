@@ -51,6 +51,7 @@ _SIGS = {
                                   _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_attn_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
     "sf_attn_default_splits": (_c_i, [_c_i, _c_i, _c_i]),
+    "sf_attn_default_splits_d": (_c_i, [_c_i, _c_i, _c_i, _c_i]),
     "sf_attn_decode_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                    _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f,
                                    _c_i, _c_p]),

@@ -924,19 +924,24 @@ extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
   return attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
 }
 
-extern "C" int sf_attn_default_splits(int B, int KVH, int T) {
-  // Up to 1024 tokens: one split (one 8-wave workgroup per kv head holds the
-  // whole cache in one round of loads; no cross-workgroup merge). Beyond:
-  // about 128 tokens per split, at most 64 splits so that the final merge's
-  // loads of the partials all go out at once. Measured on MI355X at B = 1,
-  // 2 kv heads: 32 splits for T = 4096 and 64 for T = 16384 are the fastest
-  // of 1..128.
+extern "C" int sf_attn_default_splits_d(int B, int KVH, int T, int D) {
+  // One split (one workgroup per kv head, no cross-workgroup merge) up to
+  // 1280 tokens at head_dim 64 and 640 at larger head dims: measured on MI355X
+  // at 14 / 2 heads against the split launch (head_dim 64: 9.4 against 9.9 us
+  // at 1280, 10.6 against 9.7 at 1536; head_dim 128: 10.4 against 11.0 at 640,
+  // 11.4 against 11.0 at 768). Beyond: about 128 tokens per split, at most 64
+  // splits so that the final merge's loads of the partials all go out at once
+  // (32 splits for T = 4096 and 64 for T = 16384 are the fastest of 1..128).
   (void)B;
   (void)KVH;
-  if (T <= 1024) return 1;
+  if (T <= (D <= 64 ? 1280 : 640)) return 1;
   int s = (T + 127) / 128;
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
+}
+
+extern "C" int sf_attn_default_splits(int B, int KVH, int T) {
+  return sf_attn_default_splits_d(B, KVH, T, 64);
 }
 
 static int attn_heads_per_block(int G) {
@@ -1064,7 +1069,7 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
                                    void *stream) {
   SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
              "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
-  if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T);
+  if (n_splits <= 0) n_splits = sf_attn_default_splits_d(B, KVH, T, D);
   // the reference's tiling: n_tiles = max(1, min(n_tiles, T)); tile = ceil(T / n_tiles)
   n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
   if (n_splits > kMaxSplits) n_splits = kMaxSplits;
@@ -1083,7 +1088,7 @@ extern "C" int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t 
              "invalid attention shape B=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", B, H, KVH, T_max,
              T_cap, D);
   SF_REQUIRE(T_dev, SF_EINVAL, "null pointer argument");
-  if (n_splits <= 0) n_splits = sf_attn_default_splits(B, KVH, T_max);
+  if (n_splits <= 0) n_splits = sf_attn_default_splits_d(B, KVH, T_max, D);
   return attn_launch("sf_attn_decode_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, B, H, KVH, T_add,
                      T_dev, 0, T_cap, D, scale, n_splits, stream);
@@ -1113,7 +1118,7 @@ extern "C" int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t
              "invalid prefill attention shape T_q=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", T_q, H,
              KVH, T_max, T_cap, D);
   SF_REQUIRE(T0_dev, SF_EINVAL, "null pointer argument");
-  if (n_splits <= 0) n_splits = sf_attn_default_splits(T_q, KVH, T_max);
+  if (n_splits <= 0) n_splits = sf_attn_default_splits_d(T_q, KVH, T_max, D);
   return attn_launch("sf_attn_prefill_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, T_q, H, KVH, 0,
                      T0_dev, 1, T_cap, D, scale, n_splits, stream);

@@ -83,7 +83,7 @@ def attention_decode(q: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Ten
         scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
     if n_splits is None or n_splits <= 0:
-        n_splits = int(lib.sf_attn_default_splits(B, KVH, T))
+        n_splits = int(lib.sf_attn_default_splits_d(B, KVH, T, D))
     n_splits = max(1, min(int(n_splits), max(T, 1), 512))
     ws_bytes = lib.sf_attn_workspace_bytes(B, H, D, n_splits)
     st = _lib.stream(q)

@@ -140,7 +140,7 @@ class LlamaModel:
         self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
         self.pos_dev = torch.zeros((1,), dtype=torch.int32, device=dev)
         self.hist = torch.zeros((max_seq + 1,), dtype=torch.int32, device=dev)
-        self.attn_splits = int(self.lib.sf_attn_default_splits(1, self.KVH, max_seq))
+        self.attn_splits = int(self.lib.sf_attn_default_splits_d(1, self.KVH, max_seq, self.D))
         ws = max(self.lib.sf_attn_workspace_bytes(1, self.Hq, self.D, self.attn_splits), 1 << 16)
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)   # counters start at zero
         hw = self.lib.sf_lm_head_workspace_bytes(self.V)

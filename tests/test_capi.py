@@ -97,7 +97,10 @@ def test_attention_validation_and_sizes():
     assert lib.sf_attn_default_splits(1, 2, 16384) == 64
     assert lib.sf_attn_default_splits(1, 2, 4096) == 32
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
-    assert lib.sf_attn_default_splits(1, 2, 1024) == 1 and lib.sf_attn_default_splits(1, 2, 1025) == 9
+    assert lib.sf_attn_default_splits(1, 2, 1280) == 1 and lib.sf_attn_default_splits(1, 2, 1281) == 11
+    assert lib.sf_attn_default_splits_d(1, 2, 1280, 64) == 1
+    assert lib.sf_attn_default_splits_d(1, 2, 640, 128) == 1
+    assert lib.sf_attn_default_splits_d(1, 2, 641, 128) == 6
 
 
 def test_kv_append_validation():
