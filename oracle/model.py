@@ -27,7 +27,11 @@ reference's Q4Linear computes them (fp32 activations, q4_linear.py:49-68).
 
 Pinning (tests/test_model_oracle.py): RMSNorm closed form; RoPE at position 0
 is the identity and preserves each pair's norm; attention over one cached
-token returns its V; a causal block equals the same tokens fed one by one.
+token returns its V and equals a per-row loop; a causal block equals the same
+tokens fed one by one; and the whole forward pass equals a scalar, per-element
+restatement of the reference's layers on a tiny model, which planted mistakes
+(gate and up swapped, sigmoid for SiLU, a dropped residual, RoPE on
+interleaved pairs or with the sine's sign flipped, the wrong GQA head) fail.
 """
 
 from __future__ import annotations
@@ -83,20 +87,32 @@ class KVCache:
 
 def attend(q: np.ndarray, K: np.ndarray, V: np.ndarray, pos0: int, scale: float) -> np.ndarray:
     """q [T, H, D] at positions pos0..pos0+T-1 over K, V [KVH, T_all, D]
-    (causal: row t sees keys 0..pos0+t). float64 softmax."""
+    (causal: row t sees keys 0..pos0+t; GQA head h reads kv head h // (H/KVH)).
+    float64 scores and softmax, one head at a time over all rows."""
     T, H, D = q.shape
-    KVH = K.shape[0]
+    KVH, n_all = K.shape[0], pos0 + T
     G = H // KVH
+    visible = np.arange(n_all)[None, :] <= (pos0 + np.arange(T))[:, None]  # [T, n_all]
     out = np.empty((T, H, D), np.float32)
-    for t in range(T):
-        n = pos0 + t + 1
-        for h in range(H):
-            kh = K[h // G, :n].astype(np.float64)
-            vh = V[h // G, :n].astype(np.float64)
-            s = kh @ q[t, h].astype(np.float64) * scale
-            p = np.exp(s - s.max())
-            out[t, h] = (p @ vh) / p.sum()
+    for h in range(H):
+        kh = K[h // G, :n_all].astype(np.float64)
+        vh = V[h // G, :n_all].astype(np.float64)
+        s = (q[:, h].astype(np.float64) @ kh.T) * scale
+        s = np.where(visible, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p @ vh) / p.sum(axis=1, keepdims=True)
     return out
+
+
+def swiglu(gu: np.ndarray, inter: int) -> np.ndarray:
+    """silu(gate) * up for gate|up rows [T, 2 * inter] (layers.py:143-144)."""
+    g, u = gu[:, :inter], gu[:, inter:]
+    return (g / (np.float32(1.0) + np.exp(-g))) * u
+
+
+def residual(x: np.ndarray, delta: np.ndarray) -> np.ndarray:
+    """The block's residual add (layers.py:157-163)."""
+    return x + delta
 
 
 def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: np.ndarray) -> np.ndarray:
@@ -120,12 +136,10 @@ def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: n
         k = rope(k, pos, cos_t, sin_t)
         K, V = cache.append(l, k, v.astype(np.float32))
         a = attend(q, K, V, pos0, D ** -0.5).reshape(T, Hq * D)
-        x = x + a @ L["o"].T
+        x = residual(x, a @ L["o"].T)
         xn = rmsnorm(x, L["w_post"], eps)
-        gu = xn @ L["gate_up"].T
-        g, u = gu[:, :cfg.intermediate_size], gu[:, cfg.intermediate_size:]
-        act = (g / (np.float32(1.0) + np.exp(-g))) * u
-        x = x + act @ L["down"].T
+        act = swiglu(xn @ L["gate_up"].T, cfg.intermediate_size)
+        x = residual(x, act @ L["down"].T)
     xn = rmsnorm(x, weights["norm"], eps)
     return (xn @ weights.get("lm_head", weights["embed"]).T).astype(np.float32)
 

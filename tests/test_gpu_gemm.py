@@ -47,6 +47,24 @@ def test_config2_asym_prefill(dev, N, K):
     linear.assert_close(y, linear.gemm(pk, s16(s), xk, 64, zeros=z), TOL, f"config2 [{N},{K}]")
 
 
+@pytest.mark.parametrize("N,K", [(4864, 896), (896, 4864)])
+def test_config2_hqq_packed_prefill(dev, N, K):
+    """Config 2 through the HQQ producer (siliconfer_amd/quant/hqq.py; the
+    reference packs HQQ projections with pack_weights_asym, q4_loader.py:178-183):
+    the HQQ-packed tensors differ from min-max RTN only in fp32 scale rounding
+    (one fp16-stored scale on the down shape), and the GEMM on them meets the bar."""
+    from siliconfer_amd.quant.hqq import hqq_pack
+
+    rng = np.random.default_rng(1)
+    if K == 4864:
+        laplace_outliers(rng, (4864, 896))  # the down shape is the second draw (tests/test_hqq.py)
+    W = laplace_outliers(rng, (N, K))
+    pk, s, z = hqq_pack(W, 64)
+    X = np.random.default_rng(5).normal(0, 1, (512, K)).astype(np.float32)
+    y, xk = gemm_dev(dev, pk, s, z, X, 64, torch.bfloat16)
+    linear.assert_close(y, linear.gemm(pk, s16(s), xk, 64, zeros=z), TOL, f"config2 hqq [{N},{K}]")
+
+
 @pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,N,K,g", [(33, 100, 256, 64), (200, 257, 512, 128), (130, 640, 96, 32),
                                      # groups of 96 (a group boundary inside a K step) and

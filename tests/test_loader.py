@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from siliconfer_amd.engine import (load_model, load_q4_packed, pack_and_replace_linears,
+from siliconfer_amd.engine import (Checkpoint, load_model, load_q4_packed, pack_and_replace_linears,
                                    packing_symmetry, save_q4_model)
 from siliconfer_amd.engine.q4_loader import PROJECTIONS, load_q4_model
 from siliconfer_amd.kernels import pack_weights_asym, pack_weights_sym
@@ -67,6 +67,30 @@ def test_load_model_single_and_sharded(tmp_path, shards):
     assert got["lm_head.weight"] is got["model.embed_tokens.weight"]  # tied head filled in
     for k, v in w.items():
         assert torch.equal(got[k], v), k
+
+
+@pytest.mark.parametrize("shards", [1, 3])
+def test_checkpoint_index_reads_tensors_lazily(tmp_path, shards):
+    w = tiny_checkpoint(tmp_path, shards=shards)
+    ck = Checkpoint(tmp_path)
+    assert len(ck.shards) == shards
+    assert ck.names() == sorted(w) + ["lm_head.weight"]
+    assert "lm_head.weight" in ck and "nope" not in ck
+    assert torch.equal(ck.get("lm_head.weight"), w["model.embed_tokens.weight"])
+    for k in ("model.layers.2.mlp.down_proj.weight", "model.norm.weight"):
+        assert torch.equal(ck.get(k), w[k])
+    assert dict(ck.items()).keys() == w.keys()
+    with pytest.raises(KeyError):
+        ck.get("model.layers.9.mlp.down_proj.weight")
+
+
+def test_untied_head_is_read_as_stored(tmp_path):
+    cfg = dict(TINY, tie_word_embeddings=False)
+    w = tiny_checkpoint(tmp_path, cfg=cfg)
+    c, got = load_model(tmp_path)
+    assert not c.tie_word_embeddings
+    assert got["lm_head.weight"] is not got["model.embed_tokens.weight"]
+    assert torch.equal(got["lm_head.weight"], w["lm_head.weight"])
 
 
 def test_no_bias_keeps_attention_bias_off(tmp_path):

@@ -117,3 +117,167 @@ def test_pack_sym_device_matches_numpy_packer():
     tpk, ts = pack_sym_device(torch.from_numpy(W), 64)
     np.testing.assert_array_equal(tpk.numpy(), pk)
     np.testing.assert_array_equal(ts.numpy(), s)
+
+
+# ---------------------------------------------------------------------------
+# The whole forward pass against a scalar, per-element restatement of the
+# reference's layers (/root/reference/siliconfer/model/layers.py:14-163,
+# llama.py:55-79) on a tiny model, and planted mistakes that must fail it.
+# ---------------------------------------------------------------------------
+
+TINY = ModelConfig(hidden_size=8, intermediate_size=6, num_hidden_layers=2, num_attention_heads=4,
+                   num_key_value_heads=2, head_dim=4, vocab_size=13, rms_norm_eps=1e-6,
+                   rope_theta=10000.0)
+
+
+def scalar_fixture_weights(seed=0):
+    rng = np.random.default_rng(seed)
+    c = TINY
+    H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+    rows = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
+    f = lambda *s, sd=0.5: rng.normal(0, sd, s).astype(np.float32)
+    layers = [{"qkv": f(rows, H), "qkv_bias": f(rows, sd=0.2), "o": f(H, c.num_attention_heads * D),
+               "gate_up": f(2 * I, H), "down": f(H, I), "w_in": 1 + f(H, sd=0.2),
+               "w_post": 1 + f(H, sd=0.2)} for _ in range(c.num_hidden_layers)]
+    return {"embed": f(c.vocab_size, H, sd=1.0), "norm": 1 + f(H, sd=0.2), "layers": layers}
+
+
+def _cache_dequant(vec):
+    """One cached vector as the int8 cache holds it (fp32 rule, fp16 scale)."""
+    x = np.asarray(vec, np.float32)
+    amax = np.float32(max(abs(float(v)) for v in x))
+    s = np.float32(1.0) if amax == 0 else np.float32(amax / np.float32(127))
+    codes = [max(-128, min(127, float(np.rint(np.float32(v / s))))) for v in x]
+    s16 = float(np.float32(np.float16(s)))
+    return [c * s16 for c in codes]
+
+
+def scalar_forward(W, cfg, ids, cos, sin):
+    """Token by token, element by element, in float64 (the logits of every token)."""
+    H, Hq, KVH, D, I = (cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads,
+                        cfg.head_dim, cfg.intermediate_size)
+    half, G, eps = D // 2, Hq // KVH, cfg.rms_norm_eps
+    kcache = [[[] for _ in range(KVH)] for _ in W["layers"]]
+    vcache = [[[] for _ in range(KVH)] for _ in W["layers"]]
+
+    def rms(x, w):
+        r = 1.0 / math.sqrt(sum(v * v for v in x) / len(x) + eps)
+        return [x[i] * r * float(w[i]) for i in range(len(x))]
+
+    def matvec(M, x):
+        return [sum(float(M[r][i]) * x[i] for i in range(len(x))) for r in range(len(M))]
+
+    def rot(v, p):
+        out = list(v)
+        for d in range(half):
+            c, s = float(cos[p][d]), float(sin[p][d])
+            out[d] = v[d] * c - v[d + half] * s
+            out[d + half] = v[d + half] * c + v[d] * s
+        return out
+
+    logits = []
+    for p, tok in enumerate(ids):
+        x = [float(v) for v in W["embed"][tok]]
+        for l, L in enumerate(W["layers"]):
+            qkv = [a + float(b) for a, b in zip(matvec(L["qkv"], rms(x, L["w_in"])), L["qkv_bias"])]
+            q = [rot(qkv[h * D:(h + 1) * D], p) for h in range(Hq)]
+            for h in range(KVH):
+                kcache[l][h].append(_cache_dequant(rot(qkv[(Hq + h) * D:(Hq + h + 1) * D], p)))
+                vcache[l][h].append(_cache_dequant(qkv[(Hq + KVH + h) * D:(Hq + KVH + h + 1) * D]))
+            attn = []
+            for h in range(Hq):
+                ks, vs = kcache[l][h // G], vcache[l][h // G]
+                sc = [sum(q[h][d] * k[d] for d in range(D)) / math.sqrt(D) for k in ks]
+                m = max(sc)
+                e = [math.exp(s - m) for s in sc]
+                attn += [sum(e[j] * vs[j][d] for j in range(len(e))) / sum(e) for d in range(D)]
+            x = [a + b for a, b in zip(x, matvec(L["o"], attn))]
+            gu = matvec(L["gate_up"], rms(x, L["w_post"]))
+            act = [gu[j] / (1.0 + math.exp(-gu[j])) * gu[I + j] for j in range(I)]
+            x = [a + b for a, b in zip(x, matvec(L["down"], act))]
+        logits.append(matvec(W["embed"], rms(x, W["norm"])))
+    return np.array(logits)
+
+
+def oracle_logits(W, ids):
+    cos, sin = rope_tables(TINY, 16)
+    cache = OM.KVCache(TINY.num_hidden_layers)
+    rows = [OM.forward(W, TINY, ids[:3], cache, cos, sin)]  # a causal block, then single tokens
+    for t in ids[3:]:
+        rows.append(OM.forward(W, TINY, [t], cache, cos, sin))
+    return np.concatenate(rows)
+
+
+def rel_err(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+IDS = [3, 11, 0, 7, 7, 2]
+
+
+def test_forward_equals_scalar_restatement():
+    W = scalar_fixture_weights(1)
+    cos, sin = rope_tables(TINY, 16)
+    ref = scalar_forward(W, TINY, IDS, cos, sin)
+    assert rel_err(oracle_logits(W, IDS), ref) < 1e-5
+
+
+def _rope_interleaved(x, positions, cos_t, sin_t):
+    c, s = cos_t[positions][:, None, :], sin_t[positions][:, None, :]
+    x1, x2 = x[..., 0::2], x[..., 1::2]
+    out = np.empty_like(x)
+    out[..., 0::2], out[..., 1::2] = x1 * c - x2 * s, x2 * c + x1 * s
+    return out
+
+
+ORIG_ROPE, ORIG_ATTEND = OM.rope, OM.attend
+
+
+def _attend_wrong_group(q, K, V, pos0, scale):
+    """Head h reads kv head h % KVH instead of h // (H / KVH): permute the heads
+    so the correct mapping sends each to the wrong kv head, then back."""
+    H, KVH = q.shape[1], K.shape[0]
+    G = H // KVH
+    slot = [(h % KVH) * G + h // KVH for h in range(H)]
+    qp = np.empty_like(q)
+    qp[:, slot] = q
+    return ORIG_ATTEND(qp, K, V, pos0, scale)[:, slot]
+
+
+MISTAKES = {
+    "gate_up_swapped": ("swiglu", lambda gu, I: (gu[:, I:] / (np.float32(1) + np.exp(-gu[:, I:]))) * gu[:, :I]),
+    "sigmoid_not_silu": ("swiglu", lambda gu, I: (np.float32(1) / (np.float32(1) + np.exp(-gu[:, :I]))) * gu[:, I:]),
+    "dropped_residual": ("residual", lambda x, d: d),
+    "rope_interleaved": ("rope", _rope_interleaved),
+    "rope_sin_sign": ("rope", lambda x, p, c, s: ORIG_ROPE(x, p, c, -s)),
+    "wrong_gqa_head": ("attend", _attend_wrong_group),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MISTAKES))
+def test_planted_mistakes_fail_the_bar(monkeypatch, name):
+    """Each mistake, planted in the oracle, moves the logits far past the
+    decoder's 1e-2 bar against the scalar restatement."""
+    W = scalar_fixture_weights(1)
+    cos, sin = rope_tables(TINY, 16)
+    ref = scalar_forward(W, TINY, IDS, cos, sin)
+    attr, fn = MISTAKES[name]
+    monkeypatch.setattr(OM, attr, fn)
+    assert rel_err(oracle_logits(W, IDS), ref) > 1e-2
+
+
+def test_attend_equals_per_row_loop():
+    """The vectorised causal attention against a per-(row, head) loop with its
+    own softmax, at a start offset (prefill after a cached prefix) and GQA 3:1."""
+    rng = np.random.default_rng(7)
+    T, H, KVH, D, pos0 = 5, 6, 2, 8, 4
+    q = rng.normal(0, 1, (T, H, D)).astype(np.float32)
+    K = rng.normal(0, 1, (KVH, pos0 + T, D)).astype(np.float32)
+    V = rng.normal(0, 1, (KVH, pos0 + T, D)).astype(np.float32)
+    got = OM.attend(q, K, V, pos0, 0.3)
+    for t in range(T):
+        for h in range(H):
+            k, v = K[h // 3, :pos0 + t + 1].astype(np.float64), V[h // 3, :pos0 + t + 1].astype(np.float64)
+            s = k @ q[t, h].astype(np.float64) * 0.3
+            p = np.exp(s - s.max())
+            np.testing.assert_allclose(got[t, h], p @ v / p.sum(), rtol=2e-6, atol=1e-7)
