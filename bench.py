@@ -3,9 +3,11 @@
 One step = one pass over config 3's sweep on one GPU: symmetric int4 RTN, group
 128, W in {[4096,4096], [11008,4096], [4096,11008]} x batch {1, 2, 4, 8}, fp16
 activations, fp32 accumulation — 12 GEMV launches. Every launch reads a
-different copy of its weight blob (>= 512 MB of copies per shape, twice the
-256 MB last-level cache), so the weights come from HBM. The steps are replayed
-from HIP graphs.
+different copy of its weight blob: >= 512 MB of copies per shape (twice the
+256 MB last-level cache), the four batch cases of a shape read four different
+copies and the next step the next four, so the weights come from HBM. The steps
+are replayed from HIP graphs, eight steps (96 launches) per graph where the
+step count allows.
 
 Printed JSON (one line):
   value         whole-job algorithmic GB/s: sum of per-launch algorithmic bytes
@@ -13,10 +15,13 @@ Printed JSON (one line):
                 them (inputs resident in HBM);
   roofline      the GEMV kernel: achieved = algorithmic bytes per launch /
                 average launch duration. The average comes from HIP events
-                around a graph of back-to-back launches of the same case on
-                the launch stream (an event pair around one launch has a ~6 us
-                floor of its own); `traffic` is the HBM bytes per launch that
-                rocprofv3 FETCH_SIZE + WRITE_SIZE counters measured
+                around a graph of back-to-back cold launches of the same case
+                on the launch stream (an event pair around one launch has a
+                ~6 us floor of its own); `frac_of_floor` sets the GEMV against
+                this GPU's own plain read of each case's bytes (sf_floor_read),
+                and `floor.empty_launch_us` is an empty launch, both timed the
+                same way in the same run; `traffic` is the HBM bytes per launch
+                that rocprofv3 FETCH_SIZE + WRITE_SIZE counters measured
                 (profiles/gemv_sweep_pmc.json, calibrated on a copy of known
                 size), when that file is present;
   decode_tok_s  BASELINE config 5, the metric's second half: greedy decode on a
@@ -42,7 +47,7 @@ Algorithmic bytes per launch (B = batch): N*K/2 (int4) + 2*N*K/128 (fp16
 scales) + 2*B*K (fp16 x) + 2*B*N (fp16 y).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
-       python bench.py --profile-kernels   (eager launches for rocprofv3 runs)
+       python bench.py --profile-kernels   (the sweep's graph replays, for rocprofv3 runs)
        python bench.py --profile-e2e       (eager config-5 decode steps for rocprofv3)
 """
 
@@ -141,32 +146,49 @@ class GpuSweep:
             self.n_rot = max(self.n_rot, len(blobs))
             x = torch.as_tensor(rng.normal(0, 1, (8, K)).astype(np.float16)).to(dev)
             self.keep.append(x)
-            for B in BATCHES:
+            for bi, B in enumerate(BATCHES):
                 y = torch.empty((B, N), dtype=torch.float16, device=dev)
                 self.keep.append(y)
-                self.cases.append((N, K, B, [b.data_ptr() for b in blobs], x.data_ptr(), y.data_ptr()))
+                self.cases.append((N, K, B, bi, [b.data_ptr() for b in blobs], x.data_ptr(), y.data_ptr()))
         self.step_bytes = sum(alg_bytes(N, K, B) for N, K, B, *_ in self.cases)
         self.graphs = None
 
-    def launch(self, ci: int, rot: int) -> None:
-        N, K, B, blobs, xp, yp = self.cases[ci]
-        rc = self.lib.sf_q4_gemv(blobs[rot % len(blobs)], xp, 1, yp, 1, None, None, 0, B, N, K,
+    def launch_copy(self, ci: int, copy: int) -> None:
+        N, K, B, bi, blobs, xp, yp = self.cases[ci]
+        rc = self.lib.sf_q4_gemv(blobs[copy % len(blobs)], xp, 1, yp, 1, None, None, 0, B, N, K,
                                  GROUP, 0, self.torch.cuda.current_stream().cuda_stream)
         if rc != 0:
             raise RuntimeError(self.lib.sf_last_error().decode())
+
+    def launch(self, ci: int, rot: int) -> None:
+        """Case ci in step `rot`: the four batch cases of a shape read four
+        different copies of its blob, and the next step the next four, so no
+        copy is read again before >= COLD_BYTES of other copies have been."""
+        self.launch_copy(ci, rot * len(BATCHES) + self.cases[ci][3])
 
     def eager_step(self, rot: int) -> None:
         for ci in range(len(self.cases)):
             self.launch(ci, rot)
 
+    GROUP_STEPS = 8  # steps per group graph (one replay launches 96 GEMVs)
+
     def capture(self) -> None:
+        """One graph per step rotation, and one per run of GROUP_STEPS aligned
+        rotations, so the timed loop pays one graph launch per 8 steps."""
         torch = self.torch
-        self.graphs = []
+        self.graphs, self.group_graphs = [], {}
         for rot in range(self.n_rot):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=self.stream):
                 self.eager_step(rot)
             self.graphs.append(g)
+        S = self.GROUP_STEPS
+        for r0 in range(0, self.n_rot - S + 1, S):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                for rot in range(r0, r0 + S):
+                    self.eager_step(rot)
+            self.group_graphs[r0] = g
         torch.cuda.synchronize()
 
     def step(self, i: int) -> None:
@@ -175,13 +197,54 @@ class GpuSweep:
         else:
             self.eager_step(i)
 
+    def run(self, start: int, count: int) -> None:
+        """Steps start .. start + count - 1 (rotation i % n_rot each), through
+        the group graphs where a whole aligned group fits."""
+        i, end = start, start + count
+        while i < end:
+            g = self.group_graphs.get(i % self.n_rot) if self.graphs is not None else None
+            if g is not None and end - i >= self.GROUP_STEPS:
+                g.replay()
+                i += self.GROUP_STEPS
+            else:
+                self.step(i)
+                i += 1
+
     def per_case_us(self):
         timer = Timer(self.torch, self.stream)
         out = []
-        for ci, (N, K, B, blobs, *_) in enumerate(self.cases):
-            fns = [(lambda r=r, ci=ci: self.launch(ci, r)) for r in range(len(blobs))]
+        for ci, (N, K, B, bi, blobs, *_) in enumerate(self.cases):
+            fns = [(lambda r=r, ci=ci: self.launch_copy(ci, r)) for r in range(len(blobs))]
             out.append(timer.per_call_us(fns))
         return out
+
+
+def floor_us(dev, stream, byte_counts):
+    """This GPU's per-launch floor, timed like the GEMV cases (graphs of
+    back-to-back launches between HIP events, every launch on memory no launch
+    of the last >= COLD_BYTES touched): an empty launch, and a plain read of
+    each byte count (sf_floor_read)."""
+    import torch
+
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    timer = Timer(torch, stream)
+    cur = lambda: torch.cuda.current_stream().cuda_stream
+    empty = timer.per_call_us([lambda: lib.sf_floor_empty(cur())] * 64)
+    pool_bytes = COLD_BYTES + (128 << 20)
+    pool = torch.randint(0, 256, (pool_bytes,), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    reads = {}
+    for nb in sorted(set(byte_counts)):
+        nb16 = nb // 16 * 16
+        step = -(-nb16 // 4096) * 4096
+        n = max(2, -(-COLD_BYTES // step))
+        fns = [(lambda o=(i * step) % (pool_bytes - nb16): lib.sf_floor_read(
+            pool.data_ptr() + o, nb16, sink.data_ptr(), cur())) for i in range(n)]
+        reads[nb] = timer.per_call_us(fns)
+    del pool
+    return empty, reads
 
 
 def secondary(dev, stream, eager=False):
@@ -484,8 +547,7 @@ def cpu_baseline(budget_s: float):
         return nbytes / dt / 1e9, n, dt
 
     gbs1, n1, dt1 = timed(1, kind, budget_s)
-    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(avail, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     gbsn, nn, dtn = timed(cores, "port", budget_s / 3)
     cpu_model = ""
     try:
@@ -502,30 +564,36 @@ def cpu_baseline(budget_s: float):
                   f"reference's GEMM loop of GEMVs) in {dt1:.1f} s, fp32 scales/x as the "
                   f"reference takes them",
         "all_cores": {"value": round(gbsn, 3), "cores": cores, "kind": "port",
-                      "sample": f"{nn} sweeps in {dtn:.1f} s, OpenMP row split"},
-        "cpu_model": cpu_model,
+                      "sample": f"{nn} sweeps in {dtn:.1f} s, OpenMP row split over every core "
+                                "in the process's affinity"},
+        "cpu_model": cpu_model, "nproc": os.cpu_count(),
     }
 
 
+PROFILE_WARM, PROFILE_STEPS = 8, 64
+
+
 def profile_kernels(dev) -> None:
-    """Eager launches for rocprofv3 (trace or counters): each sweep case over its
-    cold copies, a 256 MiB device copy (read 256 MiB + write 256 MiB) that
-    calibrates FETCH_SIZE / WRITE_SIZE, then the secondary kernels' cases."""
+    """The timed region's own launches for rocprofv3 (trace or counters):
+    PROFILE_WARM + PROFILE_STEPS replays of the captured sweep graphs (the
+    summary drops the warm ones), a 256 MiB device copy (read 256 MiB + write
+    256 MiB) that calibrates FETCH_SIZE / WRITE_SIZE, then the secondary
+    kernels' cases (config 1, 2, 4 and the KV append), launched once per cold
+    copy."""
     import torch
 
     sweep = GpuSweep(dev)
+    sweep.capture()
     with torch.cuda.stream(sweep.stream):
-        for ci, (N, K, B, blobs, *_) in enumerate(sweep.cases):
-            for r in range(len(blobs)):
-                sweep.launch(ci, r)
+        sweep.run(0, PROFILE_WARM + PROFILE_STEPS)
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
     torch.cuda.synchronize()
     secondary(dev, sweep.stream, eager=True)
-    print(json.dumps({"profile_kernels": [f"{N}x{K} B={B} x{len(b)}" for N, K, B, b, *_ in sweep.cases],
-                      "calibration_copy_bytes": 256 << 20}))
+    print(json.dumps({"profile_kernels": f"{PROFILE_WARM} + {PROFILE_STEPS} graph replays of the "
+                                         "12-case sweep", "calibration_copy_bytes": 256 << 20}))
 
 
 def _short_kernel(name: str) -> str:
@@ -545,35 +613,30 @@ def _short_kernel(name: str) -> str:
     return m.group(1) if m else name[:40]
 
 
-def sweep_launch_plan():
-    """(N, K, B, launches) of `--profile-kernels` in launch order: each sweep case
-    once per cold copy of its blob (the count GpuSweep's cold_copies makes)."""
-    plan = []
-    for N, K in SHAPES:
-        blob = -(-N // 16) * -(-K // 128) * 1024 + -(-N // 8) * (K // GROUP) * 16
-        n = max(2, -(-COLD_BYTES // blob))
-        plan += [(N, K, B, n) for B in BATCHES]
-    return plan
+def sweep_cases():
+    return [(N, K, B) for N, K in SHAPES for B in BATCHES]
 
 
 def summarize_profile(trace_csv=None, fetch_csv=None, write_csv=None) -> dict:
     """Summaries of rocprofv3 CSV outputs of `bench.py --profile-kernels`: the
     sweep's GEMV dispatches (the first ones of either GEMV kernel, in launch
-    order) labelled with their case by sweep_launch_plan(); per-case duration
+    order, after the warm replays) labelled with their case by position in the
+    12-launch replay; per-case duration
     stats from a --kernel-trace run, and per-case HBM bytes from FETCH_SIZE /
     WRITE_SIZE runs, scaled by what the counters read for the 256 MiB
     calibration copy (the largest copy dispatch)."""
     import csv
     import statistics
 
-    plan = sweep_launch_plan()
-    labels = [(N, K, B) for N, K, B, n in plan for _ in range(n)]
+    cs = sweep_cases()
+    skip = PROFILE_WARM * len(cs)
+    labels = [cs[i % len(cs)] for i in range(PROFILE_STEPS * len(cs))]
 
     def sweep_rows(rows, id_key):
         gemv = sorted((r for r in rows if "k_q4_gemv" in r["Kernel_Name"]), key=lambda r: int(r[id_key]))
-        return list(zip(labels, gemv[:len(labels)]))
+        return list(zip(labels, gemv[skip:skip + len(labels)]))
 
-    out = {"cases": [{"N": N, "K": K, "B": B, "launches": n} for N, K, B, n in plan]}
+    out = {"cases": [{"N": N, "K": K, "B": B, "launches": PROFILE_STEPS} for N, K, B in cs]}
     if trace_csv:
         rows = list(csv.DictReader(open(trace_csv)))
         per = {}
@@ -585,6 +648,9 @@ def summarize_profile(trace_csv=None, fetch_csv=None, write_csv=None) -> dict:
             if v:
                 c.update(kernel=k, n=len(v), mean_us=round(statistics.fmean(v), 3),
                          median_us=round(statistics.median(v), 3), min_us=round(min(v), 3))
+        means = [c["mean_us"] for c in out["cases"] if "mean_us" in c]
+        if len(means) == len(cs):
+            out["sweep_kernel_sum_us"] = round(sum(means), 3)
         copies = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
                   if "copyBuffer" in r["Kernel_Name"]]
         if copies:
@@ -665,7 +731,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of reference CPU work")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
     ap.add_argument("--profile-kernels", action="store_true",
-                    help="only run eager launches of every case (for rocprofv3)")
+                    help="only run the sweep's graph replays and the secondary kernels (for rocprofv3)")
     ap.add_argument("--summarize-e2e", metavar="CSV",
                     help="per-kernel time per token from a kernel trace of --profile-e2e")
     ap.add_argument("--summarize-profile", nargs="+", metavar="CSV",
@@ -714,14 +780,12 @@ def main() -> int:
         sweep.capture()
 
     with torch.cuda.stream(sweep.stream):
-        for i in range(args.warmup):
-            sweep.step(i)
+        sweep.run(0, args.warmup)
         torch.cuda.synchronize()
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record(sweep.stream)
-        for i in range(args.steps):
-            sweep.step(args.warmup + i)
+        sweep.run(args.warmup, args.steps)
         t1.record(sweep.stream)
         torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
@@ -731,8 +795,11 @@ def main() -> int:
     us = sweep.per_case_us()
     case_bytes = [alg_bytes(N, K, B) for N, K, B, *_ in sweep.cases]
     achieved = sum(case_bytes) / (sum(us) * 1e-6) / 1e9
+    empty_us, read_us = floor_us(dev, sweep.stream, case_bytes)
+    floor_sum = sum(read_us[b] for b in case_bytes)
     cases = [{"N": N, "K": K, "B": B, "us": round(t, 3),
-              "GBps": round(b / (t * 1e-6) / 1e9, 1)}
+              "GBps": round(b / (t * 1e-6) / 1e9, 1), "floor_us": round(read_us[b], 3),
+              "frac_of_floor": round(read_us[b] / t, 4)}
              for (N, K, B, *_), t, b in zip(sweep.cases, us, case_bytes)]
     traffic, _ = load_traffic()
     sec = None if args.no_secondary else secondary(dev, sweep.stream)
@@ -767,6 +834,14 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac_of_floor": round(floor_sum / sum(us), 4),
+            "floor": {"empty_launch_us": round(empty_us, 3),
+                      "read_GBps": round(sum(case_bytes) / (floor_sum * 1e-6) / 1e9, 1),
+                      "read_frac_of_peak": round(sum(case_bytes) / (floor_sum * 1e-6) / 1e9
+                                                 / HBM_PEAK_GBS, 4),
+                      "what": "sf_floor_read of each case's algorithmic bytes (one 16-byte load "
+                              "per lane, cold), timed like the cases in the same run; "
+                              "frac_of_floor = sum of floor times / sum of GEMV times"},
             "traffic": traffic,
             "kernel": "sf_q4_gemv (k_q4_gemv_blk: MFMA over the unit-order blob, every batch); average "
                       "over the 12 sweep cases, each timed as a graph of back-to-back cold launches "

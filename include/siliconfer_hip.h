@@ -290,6 +290,17 @@ int sf_lm_head_argmax_rows(const void *w, const void *x, int x_dtype, float *log
                            int B, int32_t *tokens_out, void *workspace, size_t workspace_bytes,
                            void *stream);
 
+/* ---- measurement floor (no counterpart in the reference: the reference only
+ * assumes a peak bandwidth, scripts/benchmark.py:26) ----------------------
+ * sf_floor_empty: one empty one-wave launch (the per-launch cost of the queue).
+ * sf_floor_read: a plain read of `bytes` (a multiple of 16, 16-byte aligned)
+ * from device memory, one 16-byte load per lane; `sink` is a device word it
+ * writes only in a case random data does not produce. bench.py times both
+ * beside the GEMV so each case's rate is reported against this GPU's own
+ * read of the same size. */
+int sf_floor_empty(void *stream);
+int sf_floor_read(const void *buf, size_t bytes, uint32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,8 @@ _SIGS = {
     "sf_lm_head_rows_workspace_bytes": (_c_sz, [_c_i, _c_i]),
     "sf_lm_head_argmax_rows": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz,
                                       _c_p]),
+    "sf_floor_empty": (_c_i, [_c_p]),
+    "sf_floor_read": (_c_i, [_c_p, _c_sz, _c_p, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -33,10 +33,14 @@
 // per MFMA).
 //
 // Work split. A workgroup owns T row tiles (16 T rows) and all of K; wave w
-// takes units [w BPW, (w + 1) BPW) of each tile. Every weight load (T x BPW per
-// lane) is issued before the first MFMA; partials are summed across the waves
-// through LDS in wave order (fixed order: bitwise repeatable, and independent
-// of T and of where the activations come from).
+// takes units [w BPW, (w + 1) BPW) of each tile. Up to 4 units per wave every
+// weight load (T x BPW per lane) is issued before the first MFMA; a longer K
+// split issues two units up front and each further unit at the top of the
+// iteration two units before its use (a wave that asks for 8+ KB at once
+// stalls on the memory pipe with its first units already in registers, and
+// computes nothing until the last of its loads has gone out). Partials are
+// summed across the waves through LDS in wave order (fixed order: bitwise
+// repeatable, and independent of T and of where the activations come from).
 // Activations come from one of two places:
 //  * XL: the workgroup stages x in LDS once (fp16 / bf16 as they are; fp32 as
 //    high and low bf16 rows; zero past K), loading it before the weight stream
@@ -333,13 +337,17 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
       }
     }
   }
+  // units issued before the first MFMA (the rest go out one per unit, PD ahead)
+  constexpr int PD = BPW >= 8 ? 2 : BPW;
   u32x4 wv[T][BPW];
-#pragma unroll
-  for (int i = 0; i < BPW; ++i)
+  auto wload = [&](int i) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
       wv[t][i] = __builtin_nontemporal_load(
           (const u32x4 *)(a.w + ((size_t)ti[t] * a.nblk + min(blk0 + i, blast)) * 1024 + lane * 16));
+  };
+#pragma unroll
+  for (int i = 0; i < PD; ++i) wload(i);
   // every load above goes out before any math (the scheduler would otherwise
   // hold some back behind the first waits to save registers)
   __builtin_amdgcn_sched_barrier(0);
@@ -402,6 +410,10 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     for (int r = 0; r < 4; ++r) acc[t][r] = 0.f;
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
+    if (i + PD < BPW) {
+      wload(i + PD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if constexpr (!XL)
       if (i + XPRE < BPW) xload(i + XPRE);
     const int kb = min(blk0 + i, blast) * kUnitK;
@@ -554,10 +566,13 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   if (wide) {
     bpw = p->nblk <= 16 ? 1 : 2;
   } else {
-    // waves per workgroup: 16 for larger batches, and for matrices with at
-    // most one workgroup per CU and a K of at least 32 units (K is then
-    // spread over more waves; measured on 4096 x 4096 and 4096 x 11008)
-    const int target = B > 4 || (p->ntiles <= 256 && p->nblk >= 32) ? 16 : 8;
+    // waves per workgroup: 16 for larger batches, for matrices with fewer row
+    // tiles than CUs and a K of at least 32 units, and for K of at least 64
+    // units (K is then spread over more waves; measured on 4096 x 11008 and
+    // 896 x 4864; 4096 x 4096, one tile per CU, runs faster at batch <= 4 on
+    // 8 waves of 4 units than on 16 of 2)
+    const int target =
+        B > 4 || (p->ntiles < 256 && p->nblk >= 32) || (p->ntiles <= 256 && p->nblk >= 64) ? 16 : 8;
     bpw = bucket((p->nblk + target - 1) / target);
   }
   const int soft = soft_max_bpw(gk, xdt != SF_F16);
