@@ -63,8 +63,7 @@ size_t sf_q4_blob_bytes(int N, int K, int group_size, int has_zeros);
 
 /* Canonical (packed u8 [N,K/2], scales f16 [N,K/g], zeros u8 [N,K/g] or NULL)
  * -> blob. has_zeros = (zeros != NULL) selects asymmetric codes. Same
- * validation as check_gemv (bindings.cpp:24-40). group_size must be a
- * multiple of 32 (SF_EUNSUPPORTED otherwise). */
+ * validation as check_gemv (bindings.cpp:24-40): any group_size dividing K. */
 int sf_q4_repack(const uint8_t *packed, const void *scales_f16, const uint8_t *zeros_u8,
                  int N, int K, int group_size, void *blob, size_t blob_bytes, void *stream);
 
@@ -80,11 +79,18 @@ int sf_q4_unpack(const void *blob, int N, int K, int group_size, int has_zeros,
  * (SF_F16 / SF_BF16 / SF_F32), and/or y_f32 [B, N]; either may be NULL but
  * not both. bias: NULL, [N] of bias_dtype (added before the store), or y_f32
  * itself (fp32: each output adds its own previous value, per batch row — a
- * residual add). fp32 accumulation throughout. K up to 16384 (8192 for group
- * sizes that are not a multiple of 64), else SF_EUNSUPPORTED. */
+ * residual add). fp32 accumulation throughout. Any K and group size the
+ * reference takes (K % group_size == 0): group sizes that are a multiple of 32
+ * run on MFMA (long K in per-wave chunks), the others — and fp32 activations
+ * whose staged rows exceed the LDS at very long K — on a VALU kernel. */
 int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
                const void *bias, int bias_dtype, int B, int N, int K, int group_size,
                int has_zeros, void *stream);
+/* 1 when sf_q4_gemv runs this shape on the MFMA GEMV in one pass over the
+ * batch, 0 when it takes the VALU kernel or batch slices (callers choosing
+ * between the batch GEMV and sf_q4_gemm for a few rows ask this). No
+ * counterpart in the reference. */
+int sf_q4_gemv_supported(int B, int N, int K, int group_size, int x_dtype);
 
 /* The decode GEMV (batch 1) with the operation that produces its input folded
  * into the activation load, for the decoder step (no counterpart in the
@@ -141,7 +147,8 @@ int sf_q4_gemv_fused_rope(const void *blob, const float *h, const float *norm_w,
 /* ---- prefill GEMM (M rows) ------------------------------------------------
  * Y[m, n] = X[m, :] . dequant(W)[n, :] for M rows; replaces q4_gemm_sym /
  * q4_gemm_asym (bindings.cpp:98-150; q4_gemm.cpp:12-51). bf16/f16 MFMA on
- * integer-valued int4 codes, fp32 per-(row, group) scale epilogue.
+ * integer-valued int4 codes, fp32 per-(row, group) scale epilogue; group sizes
+ * that are not a multiple of 32 run on the VALU kernel sf_q4_gemv uses for them.
  * workspace: sf_q4_gemm_workspace_bytes(...) bytes (may be 0 -> NULL ok). */
 size_t sf_q4_gemm_workspace_bytes(int M, int N, int K, int group_size);
 int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,

@@ -35,6 +35,7 @@ _SIGS = {
     "sf_q4_unpack": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "sf_q4_gemv": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
+    "sf_q4_gemv_supported": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i]),
     "sf_q4_gemv_fused": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_f, _c_i, _c_p, _c_i, _c_p, _c_p,
                                 _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_q4_gemv_fused_rows_supported": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),

@@ -494,9 +494,11 @@ int choose_ksplit(int M, int N, int K) {
 
 }  // namespace
 
+int sf_q4_anyg(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
+               const void *bias, int bias_dtype, int M, int N, int K, int g, int has_zeros, void *stream);
+
 extern "C" size_t sf_q4_gemm_workspace_bytes(int M, int N, int K, int group_size) {
-  (void)group_size;
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || group_size % 32) return 0;
   const int s = choose_ksplit(M, N, K);
   return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
@@ -508,8 +510,6 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
   SF_REQUIRE(M > 0 && N > 0 && K > 0 && group_size > 0, SF_EINVAL,
              "invalid shape M=%d N=%d K=%d group_size=%d", M, N, K, group_size);
   SF_REQUIRE(K % group_size == 0, SF_EINVAL, "in_features must be divisible by group_size");
-  SF_REQUIRE(group_size % 32 == 0, SF_EUNSUPPORTED,
-             "group_size=%d: this build's kernels need a multiple of 32", group_size);
   SF_REQUIRE(blob && x && (y || y_f32), SF_EINVAL, "null pointer argument");
   SF_REQUIRE(x_dtype == SF_F16 || x_dtype == SF_BF16 || x_dtype == SF_F32, SF_EINVAL,
              "bad activation dtype %d", x_dtype);
@@ -519,6 +519,9 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
              SF_EINVAL, "bad bias dtype %d", bias_dtype);
   SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)x & 15) == 0, SF_EINVAL,
              "blob must be 256-byte aligned and X 16-byte aligned");
+  if (group_size % 32)  // a group boundary inside an MFMA's k: the any-group-size kernel
+    return sf_q4_anyg(blob, x, x_dtype, y, y_dtype, y_f32, bias, bias_dtype, M, N, K, group_size,
+                      has_zeros, stream);
   BlobLayout L;
   sf_blob_layout(N, K, group_size, has_zeros, &L);
   const int ksplit = choose_ksplit(M, N, K);

@@ -22,8 +22,6 @@ void launch(const BlkPlan &p, const GemvArgs &g, int xdt, int pre, const float *
 int check_shape(int N, int K, int g) {
   SF_REQUIRE(N > 0 && K > 0 && g > 0, SF_EINVAL, "invalid shape N=%d K=%d group_size=%d", N, K, g);
   SF_REQUIRE(K % g == 0, SF_EINVAL, "in_features must be divisible by group_size");
-  SF_REQUIRE(g % 32 == 0, SF_EUNSUPPORTED,
-             "group_size=%d: this build's kernels need a multiple of 32", g);
   return SF_OK;
 }
 
@@ -46,6 +44,20 @@ GemvArgs make_args(const void *blob, const void *x, void *y, int ydt, float *y32
 
 }  // namespace
 
+int sf_q4_anyg(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
+               const void *bias, int bias_dtype, int M, int N, int K, int g, int has_zeros, void *stream);
+
+// Whether the MFMA GEMV takes this shape in one pass over the batch (the other
+// shapes run on the any-group-size kernel, or, fp32 activations, in batch
+// slices).
+extern "C" int sf_q4_gemv_supported(int B, int N, int K, int group_size, int x_dtype) {
+  if (B < 1 || B > 8 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size || group_size % 32 ||
+      (x_dtype != SF_F16 && x_dtype != SF_BF16 && x_dtype != SF_F32))
+    return 0;
+  BlkPlan p;
+  return plan_blk(B, N, K, group_size, x_dtype, PRE_NONE, false, &p) ? 1 : 0;
+}
+
 extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
                           float *y_f32, const void *bias, int bias_dtype, int B, int N, int K,
                           int group_size, int has_zeros, void *stream) {
@@ -58,6 +70,9 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
   if ((rc = check_out(y_dtype, bias, bias_dtype))) return rc;
   SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)x & 15) == 0, SF_EINVAL,
              "blob must be 256-byte aligned and x 16-byte aligned");
+  if (group_size % 32)
+    return sf_q4_anyg(blob, x, x_dtype, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, group_size,
+                      has_zeros, stream);
   const GemvArgs args =
       make_args(blob, x, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, group_size, has_zeros, stream);
   BlkPlan p;
@@ -71,10 +86,9 @@ extern "C" int sf_q4_gemv(const void *blob, const void *x, int x_dtype, void *y,
   if (x_dtype == SF_F32)
     for (int b = B - 1; b >= 1 && !bs; --b)
       if (plan_blk(b, N, K, group_size, x_dtype, PRE_NONE, false, &p)) bs = b;
-  SF_REQUIRE(bs > 0, SF_EUNSUPPORTED,
-             "in_features=%d (group_size %d) exceeds this GEMV's limit (16384; 8192 for groups "
-             "that are not a multiple of 64)",
-             K, group_size);
+  if (bs == 0)  // fp32 activations at a K whose staged rows exceed the LDS
+    return sf_q4_anyg(blob, x, x_dtype, y, y_dtype, y_f32, bias, bias_dtype, B, N, K, group_size,
+                      has_zeros, stream);
   const size_t ysz = y_dtype == SF_F32 ? 4 : 2;
   for (int b0 = 0; b0 < B; b0 += bs) {
     GemvArgs sl = args;

@@ -255,10 +255,11 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     ti[t] = min((int)blockIdx.x * T + t, a.ntiles - 1);
   }
   // K split: wave w takes uq units, one more for the first ur waves, and the
-  // last wave what is left (1 <= cnt <= BPW)
+  // last wave what is left (cnt >= 1), in chunks of BPW units: one chunk
+  // unless K exceeds what the waves' registers hold at once
   const int blk0 = wave * a.uq + min(wave, a.ur);
   const int cnt = min(a.uq + (wave < a.ur ? 1 : 0), a.nblk - blk0);
-  const int blast = blk0 + cnt - 1;  // units past the wave's own re-read its last one
+  const int nch = (cnt + BPW - 1) / BPW;
 
   uint16_t *const xl = (uint16_t *)smem;                               // XL: [rows][xp]
   const int xl_rows = XDT == SF_F32 ? 2 * B : B;
@@ -300,9 +301,26 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   __amdgpu_buffer_rsrc_t xrs;
   int xoff = 0;
   u32x4 xs[XR][4];
+  if constexpr (!XL) {
+    xrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, 0, B * K * 2, 0x00020000);
+    xoff = nl < B ? (nl * K + 8 * kg) * 2 : 0x40000000;
+  }
+  const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  const int arow = a_row<XDT>(nl, B);
+  const DequantConsts dk;
+  float acc[T][4];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.f;
+
+  for (int c = 0; c < nch; ++c) {  // wave-uniform
+  const int cb = blk0 + c * BPW, ccnt = min(BPW, cnt - c * BPW);
+  const int blast = cb + ccnt - 1;  // units past the chunk's own re-read its last one
   auto xload = [&](int i) {
     if constexpr (!XL) {
-      const int kb = min(blk0 + i, blast) * kUnitK;
+      const int kb = min(cb + i, blast) * kUnitK;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int o = kb + 32 * j + 8 * kg < K ? xoff + (kb + 32 * j) * 2 : 0x40000000;
@@ -311,8 +329,6 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     }
   };
   if constexpr (!XL) {
-    xrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, 0, B * K * 2, 0x00020000);
-    xoff = nl < B ? (nl * K + 8 * kg) * 2 : 0x40000000;
 #pragma unroll
     for (int i = 0; i < XPRE; ++i) xload(i);
   }
@@ -324,7 +340,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   uint32_t sbits[T][BPW][GS::SLOTS], zbits[T][BPW][GS::SLOTS];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int kb = min(blk0 + i, blast) * kUnitK;
+    const int kb = min(cb + i, blast) * kUnitK;
 #pragma unroll
     for (int sl = 0; sl < GS::SLOTS; ++sl) {
       const uint32_t k = (uint32_t)(kb + 32 * GS::SPAN * sl);
@@ -344,7 +360,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
       wv[t][i] = __builtin_nontemporal_load(
-          (const u32x4 *)(a.w + ((size_t)ti[t] * a.nblk + min(blk0 + i, blast)) * 1024 + lane * 16));
+          (const u32x4 *)(a.w + ((size_t)ti[t] * a.nblk + min(cb + i, blast)) * 1024 + lane * 16));
   };
 #pragma unroll
   for (int i = 0; i < PD; ++i) wload(i);
@@ -352,8 +368,8 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   // hold some back behind the first waits to save registers)
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- XL: finish the producer, stage the activations, sync
-  if constexpr (XL) {
+  // ---- XL (first chunk): finish the producer, stage the activations, sync
+  if constexpr (XL) if (c == 0) {
     if constexpr (PRE == PRE_RMSNORM) {
       const float *src = (const float *)a.x;
       for (int b = wave; b < B; b += nw) {  // uniform per wave; all lanes active
@@ -399,15 +415,6 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   }
 
   // ---- the MFMAs, unit by unit
-  const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
-  const int arow = a_row<XDT>(nl, B);
-  const DequantConsts dk;
-  float acc[T][4];
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] = 0.f;
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     if (i + PD < BPW) {
@@ -416,7 +423,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     }
     if constexpr (!XL)
       if (i + XPRE < BPW) xload(i + XPRE);
-    const int kb = min(blk0 + i, blast) * kUnitK;
+    const int kb = min(cb + i, blast) * kUnitK;
     u32x4 av[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -467,10 +474,11 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
         // units into blocks the scheduler cannot interleave (and, without the
         // staging barrier, let the compiler sink their loads into it)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = i < cnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
+        for (int r = 0; r < 4; ++r) acc[t][r] = i < ccnt ? fmaf(part[r], s, acc[t][r]) : acc[t][r];
       }
     }
   }
+  }  // K chunks
 
   // ---- fold the waves (wave order) and store
   if constexpr (XDT == SF_F32) {  // high + remainder rows: lane l (rows 4kg+r) + lane l^32 (rows 8+4kg+r)
@@ -582,6 +590,15 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   p->nw = nw;
   p->uq = bpw;  // units per wave; the last wave takes what is left
   p->ur = 0;
+  const int wmax = max_waves(pre, (p->T == 1 && pre == PRE_RMSNORM && bpw <= 2 &&
+                                   p->ntiles > 256 * (16 / (nw < kMaxWaves ? nw : kMaxWaves)) ? 2 : p->T) * bpw);
+  if (nw > wmax) {
+    // K beyond what the waves hold at once: every wave loops over chunks of
+    // BPW units, the units split as evenly as the wave count allows
+    p->nw = nw = wmax;
+    p->uq = p->nblk / nw;
+    p->ur = p->nblk % nw;
+  }
   // the folded RMSNorm's variants hold about 16 waves per CU: two row tiles
   // per workgroup when one would leave workgroups for a second round (T does
   // not change any row's summation order)

@@ -39,7 +39,15 @@ __global__ void k_repack_w(const uint8_t *__restrict__ in, uint32_t *__restrict_
     const int tile = (int)(u / NB), blk = (int)(u % NB);
     const int row = 16 * tile + (l & 15), k0 = 128 * blk + 32 * j + 8 * (l >> 4);
     uint32_t v = 0u;  // pad: code 8 (symmetric) / 0 after the mask
-    if (row < N && k0 < K) v = pair_codes(*(const uint32_t *)(in + (size_t)row * (K / 2) + k0 / 2));
+    if (row < N && k0 < K) {
+      const uint8_t *src = in + (size_t)row * (K / 2) + k0 / 2;
+      if (K % 8 == 0) {
+        v = *(const uint32_t *)src;
+      } else {  // rows are not dword-aligned: whole bytes up to K
+        for (int b = 0; b < 4 && k0 + 2 * b < K; ++b) v |= (uint32_t)src[b] << (8 * b);
+      }
+      v = pair_codes(v);
+    }
     out[o] = v ^ xor_mask;
   }
 }
@@ -47,14 +55,20 @@ __global__ void k_repack_w(const uint8_t *__restrict__ in, uint32_t *__restrict_
 // One thread per canonical dword (8 codes of one row).
 __global__ void k_unpack_w(const uint32_t *__restrict__ blob, uint8_t *__restrict__ out, int N, int K,
                            int NB, uint32_t xor_mask) {
-  const size_t total = (size_t)N * (K / 8);
+  const int per_row = (K + 7) / 8;  // dwords of 8 codes, the last one partial when K % 8
+  const size_t total = (size_t)N * per_row;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
-    const int row = (int)(o / (K / 8)), k0 = 8 * (int)(o % (K / 8));
+    const int row = (int)(o / per_row), k0 = 8 * (int)(o % per_row);
     const int blk = k0 / 128, j = (k0 % 128) / 32, kg = (k0 % 32) / 8;
     const size_t u = (size_t)(row / 16) * NB + blk;
-    const uint32_t v = blob[u * 256 + (size_t)(kg * 16 + row % 16) * 4 + j] ^ xor_mask;
-    *(uint32_t *)(out + (size_t)row * (K / 2) + k0 / 2) = unpair_codes(v);
+    const uint32_t v = unpair_codes(blob[u * 256 + (size_t)(kg * 16 + row % 16) * 4 + j] ^ xor_mask);
+    uint8_t *dst = out + (size_t)row * (K / 2) + k0 / 2;
+    if (K % 8 == 0) {
+      *(uint32_t *)dst = v;
+    } else {
+      for (int b = 0; b < 4 && k0 + 2 * b < K; ++b) dst[b] = (uint8_t)(v >> (8 * b));
+    }
   }
 }
 
@@ -104,8 +118,6 @@ int check_shape(int N, int K, int g) {
   SF_REQUIRE(N > 0 && K > 0 && g > 0, SF_EINVAL, "invalid shape N=%d K=%d group_size=%d", N, K, g);
   SF_REQUIRE(K % 2 == 0, SF_EINVAL, "W must be 2-D [out, in/2]");
   SF_REQUIRE(K % g == 0, SF_EINVAL, "in_features must be divisible by group_size");
-  SF_REQUIRE(g % 32 == 0, SF_EUNSUPPORTED,
-             "group_size=%d: this build's kernels need a multiple of 32", g);
   return SF_OK;
 }
 
@@ -163,7 +175,7 @@ extern "C" int sf_q4_unpack(const void *blob, int N, int K, int group_size, int 
   hipStream_t st = (hipStream_t)stream;
   const uint8_t *b = (const uint8_t *)blob;
   const uint32_t mask = has_zeros ? 0u : 0x88888888u;
-  k_unpack_w<<<grid_for((size_t)N * (K / 8), 256), 256, 0, st>>>((const uint32_t *)b, packed, N, K,
+  k_unpack_w<<<grid_for((size_t)N * ((K + 7) / 8), 256), 256, 0, st>>>((const uint32_t *)b, packed, N, K,
                                                                   L.NB, mask);
   size_t ns = (size_t)N * L.G;
   k_unpack_s<<<grid_for(ns, 256, 0x7fffffffu), 256, 0, st>>>((const f16 *)(b + L.s_off),

@@ -2,9 +2,11 @@
 
 `Q4Weight` owns the device blob that `sf_q4_repack` builds from the reference's
 canonical packed tensors (siliconfer/kernels/neon/__init__.py:42-81). Its
-`matmul` routes rows <= 8 to the decode GEMV and larger row counts to the MFMA
-prefill GEMM — the roles of q4_gemv_* and q4_gemm_* in the reference
-(siliconfer/kernels/neon/bindings.cpp:45-150).
+`matmul` routes rows <= 8 to the decode GEMV where its MFMA plan takes the
+shape (sf_q4_gemv_supported) and everything else to the prefill GEMM — the
+roles of q4_gemv_* and q4_gemm_* in the reference
+(siliconfer/kernels/neon/bindings.cpp:45-150). Every K and group size the
+reference takes (K % group_size == 0) computes.
 """
 
 from __future__ import annotations
@@ -110,7 +112,7 @@ class Q4Weight:
         st = _lib.stream(x)
         ydt = _lib.dt(out) if out is not None else _lib.SF_F32
         bdt = _lib.dt(bias) if bias is not None else 0
-        if M <= GEMV_MAX_ROWS:
+        if M <= GEMV_MAX_ROWS and lib.sf_q4_gemv_supported(M, N, K, g, _lib.dt(x)):
             rc = lib.sf_q4_gemv(self.blob.data_ptr(), x.data_ptr(), _lib.dt(x), _lib.ptr(out), ydt,
                                 _lib.ptr(out_f32), _lib.ptr(bias), bdt, M, N, K, g,
                                 int(self.has_zeros), st)

@@ -162,7 +162,15 @@ class LlamaModel:
         self._rows_plans = {}
         self._vbufs = None
         self._prefill_bufs = None
-        self._gemm_ws = None
+        # the prefill GEMM's split-K workspace, sized once for every projection
+        # at every chunk length up to max_prefill rows: a recorded verify graph
+        # keeps its address, so it is never replaced
+        ws = 0
+        for w in (L0.qkv, L0.o, L0.gate_up, L0.down):
+            for M in range(1, max(max_prefill, self.VERIFY_ROWS) + 1):
+                ws = max(ws, self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features,
+                                                                 w.group_size))
+        self._gemm_ws = torch.empty(ws, dtype=torch.uint8, device=dev) if ws else None
 
     # ------------------------------------------------------------------ init
     @classmethod
@@ -245,9 +253,14 @@ class LlamaModel:
                                       _lib.SF_F32, 1, w.out_features, w.in_features, w.group_size,
                                       int(w.has_zeros), self._st()), "sf_q4_gemv")
 
+    def _gemv_ok(self, M: int, w: Q4Weight) -> bool:
+        """The batch GEMV runs these rows on MFMA in one pass (sf_q4_gemv_supported)."""
+        return M <= 8 and bool(self.lib.sf_q4_gemv_supported(M, w.out_features, w.in_features,
+                                                             w.group_size, _DT[self.act_dtype]))
+
     def _gemm(self, w: Q4Weight, X: torch.Tensor, Y32: torch.Tensor, bias: torch.Tensor | None):
         M = X.shape[0]
-        if M <= 8 and w.in_features <= 16384:
+        if self._gemv_ok(M, w):
             # up to 8 rows (a short chunk, a speculative verify): the batch GEMV
             # streams the weights once for all rows
             self._chk(self.lib.sf_q4_gemv(w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], None,
@@ -258,7 +271,8 @@ class LlamaModel:
             return
         need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features, w.group_size)
         if need and (self._gemm_ws is None or self._gemm_ws.numel() < need):
-            self._gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            raise SFError(f"GEMM workspace: {need} bytes for {M} rows exceeds the preallocated "
+                          f"{0 if self._gemm_ws is None else self._gemm_ws.numel()} (max_prefill)")
         ws = self._gemm_ws if need else None
         self._chk(self.lib.sf_q4_gemm(w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], None, _lib.SF_F32,
                                       Y32.data_ptr(), None if bias is None else bias.data_ptr(),
@@ -453,7 +467,7 @@ class LlamaModel:
         same bits."""
         if T not in self._rows_plans:
             L0 = self.layers[0]
-            residual = T <= 8 and L0.o.in_features <= 16384 and L0.down.in_features <= 16384
+            residual = all(self._gemv_ok(T, w) for w in (L0.qkv, L0.o, L0.gate_up, L0.down))
             ok = lambda op, w: bool(self.fuse and residual and self.lib.sf_q4_gemv_fused_rows_supported(
                 op, T, w.out_features, w.in_features, w.group_size, int(w.has_zeros),
                 _DT[self.act_dtype]))

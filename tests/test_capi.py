@@ -59,13 +59,33 @@ def test_blob_bytes_layout():
 
 @pytest.mark.parametrize("K,g,code,msg", [
     (100, 64, -1, "in_features must be divisible by group_size"),
-    (96, 48, -2, "multiple of 32"),
+    (96, 48, -1, "null pointer argument"),   # any group size dividing K is a valid shape
+    (6, 3, -1, "null pointer argument"),
 ])
 def test_repack_rejects_bad_shapes(K, g, code, msg):
     lib = _lib.load()
     rc = lib.sf_q4_repack(None, None, None, 8, K, g, None, 0, None)
     assert rc == code
     assert msg in _lib.last_error()
+
+
+def test_gemv_support_query():
+    """sf_q4_gemv_supported: the MFMA GEMV's plans. Group sizes off the 32 grid
+    and fp32 rows too long for the LDS staging run elsewhere (still computed)."""
+    lib = _lib.load()
+    F16, BF16, F32 = _lib.SF_F16, _lib.SF_BF16, _lib.SF_F32
+    for B in (1, 2, 4, 8):
+        for N, K in [(4096, 4096), (11008, 4096), (4096, 11008), (3584, 18944), (8192, 28672)]:
+            assert lib.sf_q4_gemv_supported(B, N, K, 128, F16) == 1, (B, N, K)
+            assert lib.sf_q4_gemv_supported(B, N, K, 128, BF16) == 1, (B, N, K)
+        assert lib.sf_q4_gemv_supported(B, 896, 4864, 64, F16) == 1
+        assert lib.sf_q4_gemv_supported(B, 4096, 9216, 96, F16) == 1
+        assert lib.sf_q4_gemv_supported(B, 512, 768, 48, F16) == 0
+        assert lib.sf_q4_gemv_supported(B, 512, 768, 16, F16) == 0
+    assert lib.sf_q4_gemv_supported(1, 4096, 4096, 128, F32) == 1
+    assert lib.sf_q4_gemv_supported(1, 8192, 28672, 128, F32) == 0
+    assert lib.sf_q4_gemv_supported(9, 16, 128, 64, F16) == 0
+    assert lib.sf_q4_gemv_supported(1, 16, 100, 64, F16) == 0
 
 
 def test_gemv_rejects_batch_and_dtype():
@@ -80,8 +100,11 @@ def test_gemm_workspace_and_validation():
     lib = _lib.load()
     assert lib.sf_q4_gemm_workspace_bytes(512, 4864, 896, 64) == 0      # 152 tiles: no split
     assert lib.sf_q4_gemm_workspace_bytes(512, 896, 4864, 64) > 0       # 28 tiles: split K
+    assert lib.sf_q4_gemm_workspace_bytes(512, 896, 4848, 48) == 0      # group 48: VALU kernel
     rc = lib.sf_q4_gemm(None, None, 2, None, 2, None, None, 0, 4, 16, 96, 48, 0, None, 0, None)
-    assert rc == -2
+    assert rc == -1 and "null pointer argument" in _lib.last_error()   # a valid shape
+    rc = lib.sf_q4_gemm(None, None, 2, None, 2, None, None, 0, 4, 16, 96, 64, 0, None, 0, None)
+    assert rc == -1 and "in_features must be divisible by group_size" in _lib.last_error()
 
 
 def test_attention_validation_and_sizes():

@@ -278,3 +278,88 @@ def test_batch3to8_shapes(dev, N, K, g, asym):
         ref = linear.gemv(pk, s16(s), xk.astype(np.float64), g, zeros=z)
         linear.assert_close(y32, ref, TOL, f"N={N} K={K} g={g} asym={asym} B={B}")
         linear.assert_close(y, ref, TOL, f"fp16 out N={N} K={K} B={B}")
+
+
+# ---------------------------------------------------------------------------
+# The reference GEMV takes any K with K % g == 0 and any group size (vector
+# path plus scalar tail, /root/reference/siliconfer/kernels/neon/q4_gemv.cpp:
+# 124-134; validation only in bindings.cpp:24-40): long K runs the MFMA GEMV
+# in per-wave chunks, group sizes off the 32 grid (and fp32 rows too long for
+# the LDS) the VALU kernel. Both directly through the C ABI and through
+# Q4Weight.matmul (Q4Linear's route).
+# ---------------------------------------------------------------------------
+
+def _rand_case(rng, N, K, g, asym):
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    if asym:
+        pk, s, z = P.pack_weights_asym(W, g)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, g), None
+    return pk, s, z
+
+
+def _capi_gemv(dev, pk, s, z, x, g, xdtype):
+    from siliconfer_amd import _lib
+
+    w = Q4Weight(pk, s, z, g, device=dev)
+    xt = torch.as_tensor(x, dtype=torch.float32).to(dev).to(xdtype).contiguous()
+    B, N, K = xt.shape[0], pk.shape[0], 2 * pk.shape[1]
+    y32 = torch.empty((B, N), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.sf_q4_gemv(w.blob.data_ptr(), xt.data_ptr(), _lib.dt(xt), None, _lib.SF_F32,
+                              y32.data_ptr(), None, 0, B, N, K, g, int(z is not None),
+                              _lib.stream(xt)), "sf_q4_gemv")
+    torch.cuda.synchronize()
+    return y32.cpu().numpy(), xt.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("K", [18944, 28672])
+@pytest.mark.parametrize("B", [1, 8])
+def test_long_k_gemv(dev, xdtype, K, B):
+    """K past 16 waves x the unit cap (Qwen2.5-7B down_proj 18944, Llama-70B
+    MLP 28672; g = 128): chunked MFMA GEMV (fp32 at 28672: VALU kernel)."""
+    rng = np.random.default_rng(K + B)
+    for asym in (False, True):
+        pk, s, z = _rand_case(rng, 160, K, 128, asym)
+        x = rng.normal(0, 1, (B, K)).astype(np.float32)
+        y, xk = _capi_gemv(dev, pk, s, z, x, 128, xdtype)
+        ref = linear.gemv(pk, s16(s), xk, 128, zeros=z)
+        linear.assert_close(y, ref, TOL, f"K={K} B={B} {xdtype} asym={asym}")
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N,K,g", [(96, 768, 16), (70, 480, 48), (40, 9216, 96), (33, 90, 6),
+                                   (20, 12, 2), (17, 1000, 8)])
+def test_any_group_size(dev, xdtype, N, K, g):
+    """Group sizes that are not a multiple of 32 (a group boundary inside an
+    MFMA's 32 k), including K not a multiple of 8: GEMV at 1..8 rows through
+    the C ABI, and GEMV / GEMM rows through Q4Weight.matmul."""
+    rng = np.random.default_rng(N * K + g)
+    for asym in (False, True):
+        pk, s, z = _rand_case(rng, N, K, g, asym)
+        for B in (1, 3, 8):
+            x = rng.normal(0, 1, (B, K)).astype(np.float32)
+            y, xk = _capi_gemv(dev, pk, s, z, x, g, xdtype)
+            linear.assert_close(y, linear.gemv(pk, s16(s), xk, g, zeros=z), TOL,
+                                f"N={N} K={K} g={g} B={B} {xdtype} asym={asym}")
+        w = Q4Weight(pk, s, z, g, device=dev)
+        for M in (2, 40):
+            X = torch.as_tensor(rng.normal(0, 1, (M, K)).astype(np.float32)).to(dev).to(xdtype)
+            Y = w.matmul(X.contiguous(), out_dtype=torch.float32)
+            xk = X.float().cpu().numpy().astype(np.float64)
+            linear.assert_close(Y.cpu().numpy(), linear.gemm(pk, s16(s), xk, g, zeros=z), TOL,
+                                f"matmul M={M} g={g} {xdtype} asym={asym}")
+
+
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("N,K,g", [(70, 480, 48), (33, 90, 6), (20, 12, 2), (9, 1000, 8)])
+def test_repack_round_trip_any_group(dev, asym, N, K, g):
+    rng = np.random.default_rng(N + K + g)
+    pk, s, z = _rand_case(rng, N, K, g, asym)
+    w = Q4Weight(pk, s, z, g, device=dev)
+    pk2, s2, z2 = w.canonical()
+    np.testing.assert_array_equal(pk2.cpu().numpy(), pk)
+    np.testing.assert_array_equal(s2.cpu().numpy(), np.asarray(s, np.float32).astype(np.float16))
+    if asym:
+        np.testing.assert_array_equal(z2.cpu().numpy(), z.astype(np.uint8))
