@@ -306,7 +306,7 @@ def secondary(dev, stream, eager=False):
         n = max(2, -(-COLD_BYTES // per))
         sets = [(kc, ks, vc, vs)] + [(kc.clone(), ks.clone(), vc.clone(), vs.clone())
                                      for _ in range(n - 1)]
-        nsp = lib.sf_attn_default_splits(1, 2, T)
+        nsp = lib.sf_attn_default_splits_d(1, 2, T, 64)
         ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
         wsp = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
         fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),

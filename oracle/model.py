@@ -115,8 +115,10 @@ def residual(x: np.ndarray, delta: np.ndarray) -> np.ndarray:
     return x + delta
 
 
-def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: np.ndarray) -> np.ndarray:
-    """Run tokens `ids` (appending to `cache`) and return the logits of every row [T, V]."""
+def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: np.ndarray,
+            last_rows: int | None = None) -> np.ndarray:
+    """Run tokens `ids` (appending to `cache`) and return the logits of every
+    row [T, V], or of the last `last_rows` rows only."""
     ids = np.asarray(ids, dtype=np.int64).reshape(-1)
     T = ids.size
     H, Hq, KVH, D = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -140,6 +142,8 @@ def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: n
         xn = rmsnorm(x, L["w_post"], eps)
         act = swiglu(xn @ L["gate_up"].T, cfg.intermediate_size)
         x = residual(x, act @ L["down"].T)
+    if last_rows is not None:
+        x = x[-last_rows:]
     xn = rmsnorm(x, weights["norm"], eps)
     return (xn @ weights.get("lm_head", weights["embed"]).T).astype(np.float32)
 

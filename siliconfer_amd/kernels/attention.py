@@ -8,8 +8,8 @@ q [B, H, D]; codes int8 [B, KVH, T, D]; scales [B, KVH, T] or [B, KVH, T, 1]
 (fp32 as the reference stores them, or fp16 as this build's cache does);
 returns float32 [B, H, D]. `n_tiles` is the split-T count with the reference's
 tiling (tile = ceil(T / n_tiles)); by default this build picks its own split
-count for MI355X (`sf_attn_default_splits`) rather than `_choose_n_tiles`,
-which is kept for callers and tests that use it.
+count for MI355X (`default_splits`, which depends on the head dim) rather than
+`_choose_n_tiles`, which is kept for callers and tests that use it.
 """
 
 from __future__ import annotations
@@ -31,8 +31,11 @@ def _choose_n_tiles(T_cache: int, min_tile_size: int = 16, max_tiles: int = 256)
     return min(max_tiles, -(-T_cache // min_tile_size))
 
 
-def default_splits(B: int, n_kv_heads: int, T: int) -> int:
-    return int(_lib.load().sf_attn_default_splits(B, n_kv_heads, T))
+def default_splits(B: int, n_kv_heads: int, T: int, head_dim: int = 64) -> int:
+    """The split count `attention_decode` picks when none is given
+    (sf_attn_default_splits_d: one split up to a head_dim-dependent cache
+    length, then about 128 tokens per split)."""
+    return int(_lib.load().sf_attn_default_splits_d(B, n_kv_heads, T, head_dim))
 
 
 _workspaces: dict = {}
@@ -83,7 +86,7 @@ def attention_decode(q: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Ten
         scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
     if n_splits is None or n_splits <= 0:
-        n_splits = int(lib.sf_attn_default_splits_d(B, KVH, T, D))
+        n_splits = default_splits(B, KVH, T, D)
     n_splits = max(1, min(int(n_splits), max(T, 1), 512))
     ws_bytes = lib.sf_attn_workspace_bytes(B, H, D, n_splits)
     st = _lib.stream(q)

@@ -11,7 +11,7 @@ import torch
 
 from oracle import attention as A
 from oracle.linear import assert_close
-from siliconfer_amd.kernels.attention import (_choose_n_tiles, attention_decode,
+from siliconfer_amd.kernels.attention import (_choose_n_tiles, attention_decode, default_splits,
                                               fused_quantized_attention_decode)
 
 pytestmark = pytest.mark.gpu
@@ -205,7 +205,7 @@ def test_sixteen_heads_d128(dev, T, S):
     check(dev, *make_inputs(rng, 1, 32, 2, 128, T), n_tiles=S, what=f"G=16 D=128 T={T} S={S}")
 
 
-@pytest.mark.parametrize("T", [480, 512, 513, 545, 1024])
+@pytest.mark.parametrize("T", [480, 512, 513, 545, 1024, 1100, 1280])
 def test_one_split_wave_rounds(dev, T):
     """One split at head_dim 64 runs 16 waves, one 32-token tile each per round:
     15, 16 and 17 tiles (one wave takes a second tile), a partial last tile, and
@@ -214,3 +214,29 @@ def test_one_split_wave_rounds(dev, T):
     check(dev, *make_inputs(rng, 1, 14, 2, 64, T), n_tiles=1, what=f"one split T={T}")
     check(dev, *make_inputs(rng, 2, 14, 2, 64, T, np.float16), n_tiles=1,
           what=f"one split B=2 fp16 scales T={T}")
+
+
+@pytest.mark.parametrize("H", [14, 32])
+@pytest.mark.parametrize("T", [257, 513, 640])
+def test_one_split_head_dim_128(dev, H, T):
+    """One split at head_dim 128 (8 waves, two tiles each in flight): several
+    tile rotations, up to the default one-split limit of 640 tokens."""
+    rng = np.random.default_rng(60 + T + H)
+    check(dev, *make_inputs(rng, 1, H, 2, 128, T), n_tiles=1, what=f"D=128 H={H} one split T={T}")
+    check(dev, *make_inputs(rng, 1, H, 2, 128, T, np.float16), n_tiles=1,
+          what=f"D=128 H={H} one split fp16 scales T={T}")
+
+
+@pytest.mark.parametrize("D,T", [(64, 1280), (64, 1281), (128, 640), (128, 641)])
+def test_default_split_switch(dev, D, T):
+    """The default split count on either side of the head_dim-dependent
+    one-split limit, through attention_decode's own pick (fp32 and fp16
+    scales); default_splits reports the count it uses."""
+    assert (default_splits(1, 2, T, D) == 1) == (T <= (1280 if D == 64 else 640))
+    for sdt in (np.float32, np.float16):
+        rng = np.random.default_rng(70 + T + D)
+        q, kc, ks, vc, vs = make_inputs(rng, 1, 14, 2, D, T, sdt)
+        t = lambda a: torch.as_tensor(a).to(dev)
+        out = attention_decode(t(q), t(kc), t(ks), t(vc), t(vs)).cpu().numpy()
+        ref = A.attention_decode(q, kc, ks.astype(np.float64), vc, vs.astype(np.float64))
+        assert_close(out, ref, TOL, f"default splits D={D} T={T} {sdt.__name__}")

@@ -180,3 +180,42 @@ def test_folded_decode_equals_unfolded(dev, act):
             torch.cuda.synchronize()
             outs.append((m.logits.cpu().clone(), int(m.token.item())))
         assert torch.equal(outs[0][0], outs[1][0]) and outs[0][1] == outs[1][1]
+
+
+def test_config5_full_workload_against_oracle(dev):
+    """BASELINE config 5 as the bench runs it (bench.py e2e_model): random-init
+    Qwen2.5-0.5B geometry, seed 4, int4 sym g=64, fp16 activations, the 512-id
+    prompt, then 255 decode steps replayed from the HIP graph. The oracle runs
+    teacher-forced on the GPU's own tokens (prompt + generated, one causal
+    block, pinned equal to token-by-token decoding): every greedy token must be
+    the oracle's pick wherever its top-2 margin clears the tolerance, and the
+    logits of the prefill and of 9 spread decode steps must meet 1e-2
+    (reference harness: /root/reference/siliconfer/engine/generate.py:117-180)."""
+    cfg = ModelConfig.qwen25_05b()
+    m = LlamaModel.random_init(cfg, seed=4, group_size=64, device=dev, max_seq=512 + 256 + 256,
+                               act_dtype=torch.float16)
+    ids = np.random.default_rng(4).integers(0, cfg.vocab_size, 512)
+    m.capture(logits=True)
+    m.reset()
+    first = m.prefill(ids)
+    glog = {-1: m.logits.cpu().numpy().copy()}
+    spread = {0, 1, 2, 37, 85, 128, 170, 213, 254}
+    for i in range(255):
+        m.replay(1)
+        if i in spread:
+            torch.cuda.synchronize()
+            glog[i] = m.logits.cpu().numpy().copy()
+    toks = [first] + m.hist[512:512 + 255].cpu().tolist()
+    W = m.export_weights()
+    cos, sin = rope_tables(cfg, m.max_seq)
+    ref = OM.forward(W, cfg, np.concatenate([ids, np.asarray(toks[:-1])]), OM.KVCache(24), cos, sin,
+                     last_rows=256)
+    tol = 1e-2
+    checked = 0
+    for j in range(256):  # ref[j]: the logits after position 511 + j, which picked toks[j]
+        if margin_ok(ref[j], tol):
+            checked += 1
+            assert toks[j] == OM.greedy(ref[j]), f"config 5 token {j}"
+    assert checked >= 64, f"only {checked} of 256 steps had a clear top-2 margin"
+    for i, got in glog.items():
+        assert_close(got, ref[i + 1], tol, f"config 5 logits after decode step {i}")

@@ -197,11 +197,13 @@ def test_attention_device_length_equals_host_length(dev):
         assert_close(o1.cpu().numpy(), o2.cpu().numpy(), 1e-5, f"host vs device T={T}")
 
 
-@pytest.mark.parametrize("T0,Tq", [(0, 1), (0, 37), (20, 16)])
+@pytest.mark.parametrize("T0,Tq", [(0, 1), (0, 37), (20, 16), (0, 512), (100, 300)])
 def test_causal_prefill_attention(dev, T0, Tq):
+    """Causal prompt attention over the int8 cache, up to config 5's 512-row
+    prompt and a prompt chunk after a cached prefix."""
     lib = _lib.load()
     rng = np.random.default_rng(8 + Tq)
-    T_cap = 64
+    T_cap = max(64, T0 + Tq)
     kc, ks, vc, vs = make_cache(rng, 2, T_cap, 64)
     t = lambda a: torch.as_tensor(np.ascontiguousarray(a)).to(dev)
     q = rng.normal(0, 1, (Tq, 14, 64)).astype(np.float32)
