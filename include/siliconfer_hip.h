@@ -195,6 +195,20 @@ int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const
                         int KVH, int T, int T_cap, int D, float scale, int n_splits,
                         void *stream);
 
+/* No counterpart in the reference: sf_attn_decode_i8kv for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments and result, without the workspace: the
+ * split partials and merge counters live in a fixed device array of
+ * sf_attn_noalloc_max_bytes() (4 MiB) per GPU, held until the process ends;
+ * shapes whose workspace would exceed it (sf_attn_workspace_bytes) return
+ * SF_EINVAL. The call allocates nothing. Calls that overlap on one GPU (two
+ * streams at once) race on the shared array. */
+size_t sf_attn_noalloc_max_bytes(void);
+int sf_attn_decode_i8kv_noalloc(const void *q, int q_dtype, const int8_t *k_codes,
+                                const void *k_scales, const int8_t *v_codes, const void *v_scales,
+                                int scale_dtype, void *out, int out_dtype, int B, int H, int KVH,
+                                int T, int T_cap, int D, float scale, int n_splits, void *stream);
+
 /* The same attention with its length in device memory: T = *T_dev + T_add
  * (for decode steps replayed from a HIP graph, where the length grows by one
  * token per replay). n_splits (<= 0: sf_attn_default_splits_d at T_max) and the

@@ -56,6 +56,9 @@ _SIGS = {
     "sf_attn_decode_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                    _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f,
                                    _c_i, _c_p]),
+    "sf_attn_noalloc_max_bytes": (_c_sz, []),
+    "sf_attn_decode_i8kv_noalloc": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
+                                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_p]),
     "sf_attn_decode_i8kv_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                        _c_p, _c_sz, _c_i, _c_i, _c_i, _c_p, _c_i, _c_i, _c_i,
                                        _c_i, _c_f, _c_i, _c_p]),

@@ -26,6 +26,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "sf_common.h"
 
 namespace {
@@ -1122,4 +1124,79 @@ extern "C" int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t
   return attn_launch("sf_attn_prefill_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, T_q, H, KVH, 0,
                      T0_dev, 1, T_cap, D, scale, n_splits, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention that allocates nothing: sf_attn_decode_i8kv with its
+// workspace (split partials and merge counters) in a file-scope device array.
+// Each GPU the library runs on holds its own copy until the process ends;
+// host code reaches a device's copy only through the address
+// hipGetSymbolAddress gives for it (taken once per device, on the first call,
+// with that device current), never through the array's name. The first call
+// on a device also zeroes the counters with a fill kernel on the caller's
+// stream; every call leaves them at zero again (the merging split resets the
+// counter it used). All calls on one GPU share the array: calls that overlap
+// on one GPU (two streams at once) race.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+__global__ void k_zero_words(uint32_t *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// the current device's copy of `scratch`, set up on its first use
+int scratch_for_current_device(hipStream_t stream, void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  SF_REQUIRE(e == hipSuccess, SF_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  SF_REQUIRE(dev >= 0 && dev < kMaxDevices, SF_EUNSUPPORTED, "device %d: beyond %d devices", dev,
+             kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    SF_REQUIRE(e == hipSuccess && p, SF_EHIP, "hipGetSymbolAddress(scratch): %s",
+               hipGetErrorString(e));
+    const int words = (int)(kCounterBytes / sizeof(uint32_t));
+    k_zero_words<<<(words + 255) / 256, 256, 0, stream>>>((uint32_t *)p, words);
+    int rc = sf_check_launch("sf_attn_decode_i8kv_noalloc: zeroing the counters");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SF_OK;
+}
+
+}  // namespace
+
+extern "C" size_t sf_attn_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int sf_attn_decode_i8kv_noalloc(const void *q, int q_dtype, const int8_t *k_codes,
+                                           const void *k_scales, const int8_t *v_codes,
+                                           const void *v_scales, int scale_dtype, void *out,
+                                           int out_dtype, int B, int H, int KVH, int T, int T_cap,
+                                           int D, float scale, int n_splits, void *stream) {
+  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
+             "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
+  int s = n_splits > 0 ? n_splits : sf_attn_default_splits_d(B, KVH, T, D);
+  s = s < (T > 0 ? T : 1) ? s : (T > 0 ? T : 1);
+  const size_t need = sf_attn_workspace_bytes(B, H, D, s);
+  SF_REQUIRE(need <= kNoAllocScratchBytes, SF_EINVAL,
+             "sf_attn_decode_i8kv_noalloc: B=%d H=%d D=%d with %d splits needs %zu bytes of "
+             "scratch, more than its fixed %zu; use sf_attn_decode_i8kv with a workspace",
+             B, H, D, s, need, kNoAllocScratchBytes);
+  void *ws = nullptr;
+  int rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return sf_attn_decode_i8kv(q, q_dtype, k_codes, k_scales, v_codes, v_scales, scale_dtype, out,
+                             out_dtype, ws, kNoAllocScratchBytes, B, H, KVH, T, T_cap, D, scale, s,
+                             stream);
 }
