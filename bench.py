@@ -247,9 +247,17 @@ def floor_us(dev, stream, byte_counts):
     return empty, reads
 
 
-def secondary(dev, stream, eager=False):
-    """The other hot-path kernels at their BASELINE configs (cold HBM, graph-timed)."""
+SECONDARY_CASES = ("config1", "config2_up", "config2_down", "config4_T4096", "config4_T16384",
+                   "kv_append")
+
+
+def secondary(dev, stream, eager=False, only=None):
+    """The other hot-path kernels at their BASELINE configs (cold HBM,
+    graph-timed); `only`: a subset of SECONDARY_CASES (the per-case rocprofv3
+    runs time one case alone)."""
     import torch
+
+    want = lambda name: only is None or name in only
 
     from siliconfer_amd import _lib
     from siliconfer_amd.kernels import Q4Weight, pack_weights_asym
@@ -261,6 +269,27 @@ def secondary(dev, stream, eager=False):
     rng = np.random.default_rng(0)
 
     # config 1: [4864, 896] sym g=64, B=1
+    if want("config1"):
+        _config1(dev, lib, timer, cur, rng, out)
+    # config 2: asym prefill GEMM, X bf16 [512, K], up/gate [4864, 896] and down [896, 4864]
+    for name, (N, K) in (("config2_up", (4864, 896)), ("config2_down", (896, 4864))):
+        W = rng.laplace(0, 0.015, (N, K)).astype(np.float32)
+        if want(name):
+            _config2(dev, lib, timer, cur, rng, out, N, K, W)
+    # config 4: decode attention over an int8 cache, fp16 scales, q fp16 [1, 14, 64]
+    for T in (4096, 16384):
+        if want(f"config4_T{T}"):
+            _config4(dev, lib, timer, cur, out, T)
+    if want("kv_append"):
+        _kv_append(dev, lib, timer, cur, out)
+    return out
+
+
+def _config1(dev, lib, timer, cur, rng, out):
+    import torch
+
+    from siliconfer_amd.kernels import Q4Weight
+
     pk, s = quantize_shape(4864, 896, 0, g=64)
     w = Q4Weight(pk, s, None, 64, device=dev)
     blobs = cold_copies(w.blob, w.nbytes)
@@ -272,55 +301,61 @@ def secondary(dev, stream, eager=False):
     nb = alg_bytes(4864, 896, 1, 64)
     out["config1_gemv_4864x896_g64_b1"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
                                            "bytes": nb}
-    del blobs, w
 
-    # config 2: asym prefill GEMM, X bf16 [512, K], up/gate [4864, 896] and down [896, 4864]
-    for (N, K) in [(4864, 896), (896, 4864)]:
-        W = rng.laplace(0, 0.015, (N, K)).astype(np.float32)
-        pa, sa, za = pack_weights_asym(W, 64)
-        wq = Q4Weight(pa, sa, za, 64, device=dev)
-        X = torch.as_tensor(rng.normal(0, 1, (512, K)).astype(np.float32)).to(dev).to(torch.bfloat16)
-        Y = torch.empty((512, N), dtype=torch.bfloat16, device=dev)
-        wsb = lib.sf_q4_gemm_workspace_bytes(512, N, K, 64)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
-        blobs = cold_copies(wq.blob, wq.nbytes)
-        fns = [(lambda b=b: lib.sf_q4_gemm(b.data_ptr(), X.data_ptr(), 2, Y.data_ptr(), 2, None, None,
-                                           0, 512, N, K, 64, 1, ws.data_ptr() if wsb else None, wsb,
-                                           cur())) for b in blobs]
-        us = timer.per_call_us(fns, reps=2)
-        flops = 2.0 * 512 * N * K
-        out[f"config2_gemm_asym_m512_{N}x{K}"] = {
-            "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
-            "mfma_frac_of_bf16_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
-        del blobs, wq
 
-    # config 4: decode attention over an int8 cache, fp16 scales, q fp16 [1, 14, 64]
-    for T in (4096, 16384):
-        kc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
-        vc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
-        ks = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
-        vs = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
-        q = torch.randn((1, 14, 64), device=dev).half()
-        o = torch.empty((1, 14, 64), dtype=torch.float16, device=dev)
-        per = kc.numel() * 2 + ks.numel() * 4
-        n = max(2, -(-COLD_BYTES // per))
-        sets = [(kc, ks, vc, vs)] + [(kc.clone(), ks.clone(), vc.clone(), vs.clone())
-                                     for _ in range(n - 1)]
-        nsp = lib.sf_attn_default_splits_d(1, 2, T, 64)
-        ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
-        wsp = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
-        fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
-                                                    a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
-                                                    1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
-                                                    0.125, nsp, cur())) for a in sets]
-        us = timer.per_call_us(fns)
-        nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
-        out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
-                                     "bytes": nb, "splits": nsp,
-                                     "launches": "one (splits + fused merge)"}
-        del sets
+def _config2(dev, lib, timer, cur, rng, out, N, K, W):
+    import torch
 
-    # KV append: one decode token, [1, 2, 1, 64] fp16 K and V into a 4096-slot cache
+    from siliconfer_amd.kernels import Q4Weight, pack_weights_asym
+
+    pa, sa, za = pack_weights_asym(W, 64)
+    wq = Q4Weight(pa, sa, za, 64, device=dev)
+    X = torch.as_tensor(rng.normal(0, 1, (512, K)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    Y = torch.empty((512, N), dtype=torch.bfloat16, device=dev)
+    wsb = lib.sf_q4_gemm_workspace_bytes(512, N, K, 64)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    blobs = cold_copies(wq.blob, wq.nbytes)
+    fns = [(lambda b=b: lib.sf_q4_gemm(b.data_ptr(), X.data_ptr(), 2, Y.data_ptr(), 2, None, None,
+                                       0, 512, N, K, 64, 1, ws.data_ptr() if wsb else None, wsb,
+                                       cur())) for b in blobs]
+    us = timer.per_call_us(fns, reps=2)
+    flops = 2.0 * 512 * N * K
+    out[f"config2_gemm_asym_m512_{N}x{K}"] = {
+        "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
+        "mfma_frac_of_bf16_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
+def _config4(dev, lib, timer, cur, out, T):
+    import torch
+
+    kc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
+    vc = torch.randint(-127, 128, (1, 2, T, 64), dtype=torch.int8, device=dev)
+    ks = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+    vs = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+    q = torch.randn((1, 14, 64), device=dev).half()
+    o = torch.empty((1, 14, 64), dtype=torch.float16, device=dev)
+    per = kc.numel() * 2 + ks.numel() * 4
+    n = max(2, -(-COLD_BYTES // per))
+    sets = [(kc, ks, vc, vs)] + [(kc.clone(), ks.clone(), vc.clone(), vs.clone())
+                                 for _ in range(n - 1)]
+    nsp = lib.sf_attn_default_splits_d(1, 2, T, 64)
+    ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
+    wsp = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
+    fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
+                                                a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
+                                                1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
+                                                0.125, nsp, cur())) for a in sets]
+    us = timer.per_call_us(fns)
+    nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
+    out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
+                                 "bytes": nb, "splits": nsp,
+                                 "launches": "one (splits + fused merge)"}
+
+
+def _kv_append(dev, lib, timer, cur, out):
+    """KV append: one decode token, [1, 2, 1, 64] fp16 K and V into a 4096-slot cache."""
+    import torch
+
     qk = torch.empty((1, 2, 4096, 64), dtype=torch.int8, device=dev)
     sk = torch.empty((1, 2, 4096), dtype=torch.float16, device=dev)
     qv, sv = torch.empty_like(qk), torch.empty_like(sk)
@@ -330,7 +365,6 @@ def secondary(dev, stream, eager=False):
                                                sk.data_ptr(), qv.data_ptr(), sv.data_ptr(), 1, 1, 2,
                                                1, t, 4096, 64, cur())) for t in range(64)]
     out["kv_append_1tok_2heads_d64"] = {"us": round(timer.per_call_us(fns), 3)}
-    return out
 
 
 E2E_PROMPT, E2E_TOKENS = 512, 256
@@ -367,6 +401,18 @@ def e2e_decode(dev, runs: int = 3):
         med = rs[order[runs // 2]]
         timer = Timer(torch, torch.cuda.Stream(dev))
         head_us = timer.per_call_us([lambda: m._lm_head_norm(m.h, m.token, None, logits=False)] * 32)
+        # the prompt's causal attention alone: every layer's call on its own cache
+        from siliconfer_amd import _lib
+        lib = _lib.load()
+        Qp = torch.randn((E2E_PROMPT, m.Hq, m.D), device=dev).to(act)
+        Ap = torch.empty((E2E_PROMPT, m.Hq * m.D), dtype=act, device=dev)
+        cur = lambda: torch.cuda.current_stream().cuda_stream
+        pf_fns = [(lambda l=l: lib.sf_attn_prefill_i8kv(
+            Qp.data_ptr(), _lib.dt(Qp), m.k_codes[l].data_ptr(), m.k_scales[l].data_ptr(),
+            m.v_codes[l].data_ptr(), m.v_scales[l].data_ptr(), _lib.SF_F16, Ap.data_ptr(), _lib.dt(Ap),
+            E2E_PROMPT, m.Hq, m.KVH, 0, m.max_seq, m.D, m.scale, cur()))
+            for l in range(cfg.num_hidden_layers)]
+        pf_attn_ms = timer.per_call_us(pf_fns) * cfg.num_hidden_layers * 1e-3
         w_bytes = sum(getattr(L, n).nbytes for L in m.layers for n in ("qkv", "o", "gate_up", "down"))
         head_bytes = m.embed.numel() * 2
         T_mean = E2E_PROMPT + E2E_TOKENS / 2
@@ -378,6 +424,8 @@ def e2e_decode(dev, runs: int = 3):
             "runs_tok_s": [round(r.decode_tok_s, 1) for r in rs],
             "ms_per_token": round(ms, 4),
             "prefill_ms_512": round(med.prefill_time * 1e3, 3),
+            "prefill_attention_ms_512": round(pf_attn_ms, 3),
+            "prefill_attention_share": round(pf_attn_ms / (med.prefill_time * 1e3), 4),
             "lm_head_us": round(head_us, 2),
             "lm_head_share": round(head_us * 1e-3 / ms, 4),
             "hbm_bytes_per_token": int(per_tok),
@@ -730,6 +778,8 @@ def main() -> int:
     ap.add_argument("--no-spec", action="store_true", help="skip the speculative-decoding leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of reference CPU work")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of HIP graphs")
+    ap.add_argument("--profile-case", choices=SECONDARY_CASES,
+                    help="only time one secondary case (its graph replays, for rocprofv3)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the sweep's graph replays and the secondary kernels (for rocprofv3)")
     ap.add_argument("--summarize-e2e", metavar="CSV",
@@ -759,6 +809,10 @@ def main() -> int:
         raise SystemExit("bench.py needs a gfx950 GPU and the built libsiliconfer_hip.so")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.profile_case:
+        st = torch.cuda.Stream(dev)
+        print(json.dumps(secondary(dev, st, only={args.profile_case})))
+        return 0
     if args.profile_kernels:
         profile_kernels(dev)
         return 0

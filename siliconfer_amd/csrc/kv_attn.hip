@@ -859,6 +859,218 @@ int pow2_log2_at_least(int v) {
   return l;
 }
 
+// ---------------------------------------------------------------------------
+// causal prefill attention, flash style on MFMA
+// ---------------------------------------------------------------------------
+// The prompt's query rows of one kv head are the (token, head) pairs
+// c = t * G + h; each wave owns 16 consecutive ones as the 16 MFMA columns
+// and walks the key tiles 0, 32, 64, ... up to the causal limit of its last
+// row, keeping each row's online softmax (base 2) as the decode kernel keeps
+// each head's: S^T = K Q^T (K codes -> exact fp16 as the A operand, the rows'
+// q as the B operand, fp16 hi + lo for fp32 / bf16 q), a key past a row's
+// own limit T0 + t + 1 weighs exactly 0, and O^T = V^T P^T takes P^T from the
+// S^T registers (V scale folded, hi + lo) and V^T from the wave's LDS stage
+// through ds_read_b64_tr_b8. Each row's result is final in its wave: no merge
+// across waves or workgroups, no barrier. Every K / V tile is read once per
+// wave (16 query rows), not once per query row.
+constexpr int kPfWaves = 4;
+
+template <int QDT, int SDT, int D>
+__global__ void __launch_bounds__(kPfWaves * 64)
+k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
+                    const void *__restrict__ ks, const int8_t *__restrict__ vc,
+                    const void *__restrict__ vs, void *__restrict__ out, int odt, int H, int KVH,
+                    int T_q, int T0, const int *__restrict__ T0_dev, int T_cap, float qscale,
+                    int vscale) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int NW = kPfWaves, NB = 2;
+  constexpr int KS = D / 32, DB = D / 16, KW = D / 16, VC = D / 32, PITCH = D + 8;
+  constexpr bool QSPLIT = QDT != SF_F16;
+  __shared__ __attribute__((aligned(16))) float smem[NW * 32 * PITCH / 4];
+
+  const int kvh = blockIdx.y;
+  const int G = H / KVH;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hl = lane & 15, g = lane >> 4;
+  const int ncol = T_q * G;
+  const int c0 = (blockIdx.x * NW + wave) * 16;
+  if (c0 >= ncol) return;  // wave-uniform; nothing below waits on other waves
+  const int start = T0_dev ? *T0_dev : T0;
+  const int c = min(c0 + hl, ncol - 1);  // columns past the rows repeat the last one (not stored)
+  const int tq = c / G, hh = c - tq * G;
+  const int lim = max(0, min(start + tq + 1, T_cap));             // keys this row sees
+  const int t1 = max(0, min(start + (min(c0 + 15, ncol - 1) / G) + 1, T_cap));  // the wave's last row's
+  const size_t base = (size_t)kvh * T_cap;
+  const size_t qrow = (size_t)tq * H + (size_t)kvh * G + hh;
+
+  half8_t qh[KS], ql[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    float f[8];
+    sf_load8_as_f32<QDT>(q, qrow * D + g * (D / 4) + 8 * k, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qh[k][i] = (f16)f[i];
+      ql[k][i] = (f16)(f[i] - (float)qh[k][i]);
+    }
+  }
+
+  struct Tile {
+    u32x4 k[2][KW / 4];
+    u32x4 v[VC];
+    float ks[8], vs[8];
+  };
+  const int ntiles = (t1 + 31) / 32;
+  auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
+  auto load = [&](int j, Tile &tl) {
+    const int tb = 32 * j;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int t = min(tb + 16 * h2 + hl, t1 - 1);
+      const u32x4 *kp = (const u32x4 *)(kc + (base + t) * D + g * (D / 4));
+#pragma unroll
+      for (int cc = 0; cc < KW / 4; ++cc) tl.k[h2][cc] = kp[cc];
+    }
+#pragma unroll
+    for (int cc = 0; cc < VC; ++cc) {
+      const int ch = lane + 64 * cc, tok = ch / (D / 16), piece = ch % (D / 16);
+      const int t = min(tb + tok, t1 - 1);
+      tl.v[cc] = *(const u32x4 *)(vc + (base + t) * D + piece * 16);
+    }
+    if (vscale) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const size_t row = base + min(tb + 16 * h2 + 4 * g, T_cap - 4);
+        if constexpr (SDT == SF_F16) {
+          const u32x2 a = *(const u32x2 *)((const f16 *)ks + row);
+          const u32x2 b2 = *(const u32x2 *)((const f16 *)vs + row);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const half2_t ka = sf_bitcast<half2_t>(a[i]), va = sf_bitcast<half2_t>(b2[i]);
+            tl.ks[4 * h2 + 2 * i] = (float)ka.x;
+            tl.ks[4 * h2 + 2 * i + 1] = (float)ka.y;
+            tl.vs[4 * h2 + 2 * i] = (float)va.x;
+            tl.vs[4 * h2 + 2 * i + 1] = (float)va.y;
+          }
+        } else {
+          const float4_t a = *(const float4_t *)((const float *)ks + row);
+          const float4_t b2 = *(const float4_t *)((const float *)vs + row);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            tl.ks[4 * h2 + i] = a[i];
+            tl.vs[4 * h2 + i] = b2[i];
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const size_t row = base + min(tb + tok_of(r), t1 - 1);
+        tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
+        tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
+      }
+    }
+  };
+
+  uint8_t *vt = (uint8_t *)smem + wave * 32 * PITCH;
+  float m = -INFINITY, lsum = 0.f;
+  float4_t O[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) O[d] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int j, const Tile &tl) {
+    const int tb = 32 * j;
+    float4_t S[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      S[h2] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const u32x4 w = tl.k[h2][k / 2];
+        const half8_t a = (k & 1) ? i8x8_to_h8(w.z, w.w) : i8x8_to_h8(w.x, w.y);
+        S[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[k], S[h2], 0, 0, 0);
+        if constexpr (QSPLIT) S[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[k], S[h2], 0, 0, 0);
+      }
+    }
+    float sc[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const bool valid = tb + tok_of(r) < lim;
+      sc[r] = valid ? S[r >> 2][r & 3] * (tl.ks[r] * qscale) : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float cf = __builtin_amdgcn_exp2f(m - m_ref);
+    m = m_new;
+    half8_t ph, pl;
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const bool valid = tb + tok_of(r) < lim;
+      const float p = valid ? __builtin_amdgcn_exp2f(sc[r] - m_ref) : 0.f;
+      ps += p;
+      // masked keys weigh exactly 0 (a scale past the cached length may be any value)
+      const float pv = valid ? p * tl.vs[r] : 0.f;
+      ph[r] = (f16)pv;
+      pl[r] = (f16)(pv - (float)ph[r]);
+    }
+    lsum = fmaf(lsum, cf, ps);
+#pragma unroll
+    for (int cc = 0; cc < VC; ++cc) {
+      const int ch = lane + 64 * cc, tok = ch / (D / 16), piece = ch % (D / 16);
+      uint2 *dst = (uint2 *)(vt + tok * PITCH + piece * 16);
+      dst[0] = uint2{tl.v[cc].x, tl.v[cc].y};
+      dst[1] = uint2{tl.v[cc].z, tl.v[cc].w};
+    }
+    const int vtok = tok_of(hl >> 1);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      typedef int v2i __attribute__((ext_vector_type(2)));
+      const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i *)(vt + vtok * PITCH + 16 * d + 8 * (hl & 1)));
+      const half8_t a = i8x8_to_h8((uint32_t)r.x, (uint32_t)r.y);
+      O[d] *= cf;
+      O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, O[d], 0, 0, 0);
+      O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, O[d], 0, 0, 0);
+    }
+  };
+
+  Tile tl[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (u < ntiles) load(u, tl[u]);
+  for (int i0 = 0; i0 < ntiles; i0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int i = i0 + u;
+      if (i < ntiles) {
+        compute(i, tl[u]);
+        if (i + NB < ntiles) load(i + NB, tl[u]);
+      }
+    }
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (c0 + hl >= ncol) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const size_t o = qrow * D;
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = O[d][i] * inv;
+      const size_t idx = o + 16 * d + 4 * g + i;
+      if (odt == SF_F32) ((float *)out)[idx] = v;
+      else if (odt == SF_F16) ((f16 *)out)[idx] = (f16)v;
+      else ((uint16_t *)out)[idx] = sf_f32_to_bf16(v);
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1096,6 +1308,64 @@ extern "C" int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t 
                      T_dev, 0, T_cap, D, scale, n_splits, stream);
 }
 
+// Flash-style prefill (k_attn_prefill_mfma) for prompt chunks of kPfMinRows
+// rows or more at head_dim 64 / 128; shorter chunks (speculative verify rows)
+// keep the split-T decode kernel, which spreads a long cache over workgroups.
+constexpr int kPfMinRows = 16;
+
+static bool prefill_mfma_ok(int T_q, int H, int KVH, int D, const int8_t *k_codes,
+                            const int8_t *v_codes) {
+  const char *mfma_env = getenv("SF_ATTN_MFMA");
+  const bool mfma_ok = !(mfma_env && mfma_env[0] == '0');
+  return mfma_ok && T_q >= kPfMinRows && H % KVH == 0 && (D == 64 || D == 128) &&
+         (((uintptr_t)k_codes | (uintptr_t)v_codes) & 15) == 0;
+}
+
+static int prefill_mfma_launch(const char *what, const void *q, int q_dtype, const int8_t *k_codes,
+                               const void *k_scales, const int8_t *v_codes, const void *v_scales,
+                               int scale_dtype, void *out, int out_dtype, int T_q, int H, int KVH,
+                               int T0, const int *T0_dev, int T_cap, int D, float scale,
+                               void *stream) {
+  SF_REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out, SF_EINVAL,
+             "null pointer argument");
+  SF_REQUIRE(q_dtype >= SF_F32 && q_dtype <= SF_BF16 && out_dtype >= SF_F32 && out_dtype <= SF_BF16,
+             SF_EINVAL, "bad q/out dtype");
+  SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
+             scale_dtype);
+  SF_REQUIRE(((uintptr_t)q & 15) == 0, SF_EINVAL, "q must be 16-byte aligned");
+  const int G = H / KVH;
+  const float qscale = scale * 1.4426950408889634f;
+  const size_t sal = scale_dtype == SF_F16 ? 8 : 16;
+  const int vscale = T_cap % 4 == 0 && T_cap >= 4 && (uintptr_t)k_scales % sal == 0 &&
+                     (uintptr_t)v_scales % sal == 0;
+  const long long ncol = (long long)T_q * G;
+  const long long nblk = (ncol + 16 * kPfWaves - 1) / (16 * kPfWaves);
+  SF_REQUIRE(nblk <= 0x7fffffff, SF_EINVAL, "prefill of %d rows is too long", T_q);
+  dim3 grid((unsigned)nblk, KVH, 1);
+  hipStream_t st = (hipStream_t)stream;
+#define SF_PF_LAUNCH(QD, SD, DD)                                                               \
+  k_attn_prefill_mfma<QD, SD, DD><<<grid, kPfWaves * 64, 0, st>>>(                            \
+      q, k_codes, k_scales, v_codes, v_scales, out, out_dtype, H, KVH, T_q, T0, T0_dev, T_cap, \
+      qscale, vscale)
+#define SF_PF_D(QD, SD)                  \
+  do {                                   \
+    if (D == 64) SF_PF_LAUNCH(QD, SD, 64); \
+    else SF_PF_LAUNCH(QD, SD, 128);      \
+  } while (0)
+  if (scale_dtype == SF_F16) {
+    if (q_dtype == SF_F32) SF_PF_D(SF_F32, SF_F16);
+    else if (q_dtype == SF_F16) SF_PF_D(SF_F16, SF_F16);
+    else SF_PF_D(SF_BF16, SF_F16);
+  } else {
+    if (q_dtype == SF_F32) SF_PF_D(SF_F32, SF_F32);
+    else if (q_dtype == SF_F16) SF_PF_D(SF_F16, SF_F32);
+    else SF_PF_D(SF_BF16, SF_F32);
+  }
+#undef SF_PF_D
+#undef SF_PF_LAUNCH
+  return sf_check_launch(what);
+}
+
 extern "C" int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
                                     const void *k_scales, const int8_t *v_codes,
                                     const void *v_scales, int scale_dtype, void *out,
@@ -1104,6 +1374,10 @@ extern "C" int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_
   SF_REQUIRE(T_q > 0 && H > 0 && KVH > 0 && D > 0 && T0 >= 0 && T0 + T_q <= T_cap, SF_EINVAL,
              "invalid prefill attention shape T_q=%d H=%d KVH=%d T0=%d T_cap=%d D=%d", T_q, H, KVH,
              T0, T_cap, D);
+  if (prefill_mfma_ok(T_q, H, KVH, D, k_codes, v_codes))
+    return prefill_mfma_launch("sf_attn_prefill_i8kv", q, q_dtype, k_codes, k_scales, v_codes,
+                               v_scales, scale_dtype, out, out_dtype, T_q, H, KVH, T0, nullptr,
+                               T_cap, D, scale, stream);
   return attn_launch("sf_attn_prefill_i8kv", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, nullptr, 0, T_q, H, KVH, T0, nullptr, 1, T_cap, D,
                      scale, 1, stream);
@@ -1120,6 +1394,10 @@ extern "C" int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t
              "invalid prefill attention shape T_q=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", T_q, H,
              KVH, T_max, T_cap, D);
   SF_REQUIRE(T0_dev, SF_EINVAL, "null pointer argument");
+  if (prefill_mfma_ok(T_q, H, KVH, D, k_codes, v_codes))
+    return prefill_mfma_launch("sf_attn_prefill_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes,
+                               v_scales, scale_dtype, out, out_dtype, T_q, H, KVH, 0, T0_dev, T_cap,
+                               D, scale, stream);
   if (n_splits <= 0) n_splits = sf_attn_default_splits_d(T_q, KVH, T_max, D);
   return attn_launch("sf_attn_prefill_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, T_q, H, KVH, 0,

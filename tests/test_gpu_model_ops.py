@@ -217,3 +217,37 @@ def test_causal_prefill_attention(dev, T0, Tq):
     V = (vc[0].astype(np.float32) * vs[0][..., None])
     ref = OM.attend(q, K, V, T0, 0.125)
     assert_close(out.cpu().numpy(), ref, 2e-3, f"prefill T0={T0} Tq={Tq}")
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("D,H,KVH,T0,Tq,T_cap", [
+    (64, 14, 2, 0, 16, 16),       # the smallest flash chunk, cache exactly full
+    (64, 14, 2, 5, 333, 341),     # T_cap % 4 != 0 (per-token scale loads)
+    (128, 32, 2, 0, 100, 128),    # 16 query heads per kv head, head_dim 128
+    (128, 8, 8, 40, 70, 112),     # MHA
+    (64, 16, 2, 7, 257, 300),     # 8 heads per kv head, rows not a multiple of 16
+])
+@pytest.mark.parametrize("qdt,sdt", [(torch.float32, np.float32), (torch.float16, np.float16),
+                                     (torch.bfloat16, np.float16)])
+def test_prefill_attention_shapes(dev, monkeypatch, kernel, D, H, KVH, T0, Tq, T_cap, qdt, sdt):
+    """Causal prefill attention (the flash MFMA kernel for prompt chunks of 16+
+    rows at head_dim 64 / 128; SF_ATTN_MFMA=0 keeps the split-T decode kernel)
+    against the oracle's causal attention over the dequantized int8 cache."""
+    monkeypatch.setenv("SF_ATTN_MFMA", "1" if kernel == "mfma" else "0")
+    lib = _lib.load()
+    rng = np.random.default_rng(D + H + Tq)
+    kc, ks, vc, vs = make_cache(rng, KVH, T_cap, D)
+    ks, vs = ks.astype(sdt), vs.astype(sdt)
+    t = lambda a: torch.as_tensor(np.ascontiguousarray(a)).to(dev)
+    q = t(rng.normal(0, 1, (Tq, H, D)).astype(np.float32)).to(qdt)
+    out = torch.empty((Tq, H, D), dtype=torch.float32, device=dev)
+    kcd, ksd, vcd, vsd = t(kc), t(ks), t(vc), t(vs)
+    sdt_code = F16 if sdt == np.float16 else F32
+    _lib.check(lib.sf_attn_prefill_i8kv(q.data_ptr(), _lib.dt(q), kcd.data_ptr(), ksd.data_ptr(),
+                                        vcd.data_ptr(), vsd.data_ptr(), sdt_code, out.data_ptr(), F32,
+                                        Tq, H, KVH, T0, T_cap, D, D ** -0.5, st()), "prefill")
+    torch.cuda.synchronize()
+    K = kc[0].astype(np.float32) * ks[0].astype(np.float32)[..., None]
+    V = vc[0].astype(np.float32) * vs[0].astype(np.float32)[..., None]
+    ref = OM.attend(q.float().cpu().numpy(), K, V, T0, D ** -0.5)
+    assert_close(out.cpu().numpy(), ref, 2e-3, f"prefill {kernel} D={D} H={H}/{KVH} T0={T0} Tq={Tq}")
