@@ -227,7 +227,9 @@ __host__ __device__ constexpr int max_waves(int pre, int t_bpw) {
   return pre == PRE_RMSNORM && t_bpw > 4 ? 8 : kMaxWaves;
 }
 
-template <int XDT, bool ASYM, int GK, int T, int BPW, bool XL, int PRE, bool ROPE>
+// KC: the K split loops over chunks of BPW units (K beyond what the waves
+// hold at once); the other variants compile with one chunk as straight-line code.
+template <int XDT, bool ASYM, int GK, int T, int BPW, bool XL, int PRE, bool ROPE, bool KC>
 __global__ void __launch_bounds__(max_waves(PRE, T * BPW) * 64)
 k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   static_assert(XL || (PRE == PRE_NONE && XDT != SF_F32), "folded producers and fp32 activations stage in LDS");
@@ -259,7 +261,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   // unless K exceeds what the waves' registers hold at once
   const int blk0 = wave * a.uq + min(wave, a.ur);
   const int cnt = min(a.uq + (wave < a.ur ? 1 : 0), a.nblk - blk0);
-  const int nch = (cnt + BPW - 1) / BPW;
+  const int nch = KC ? (cnt + BPW - 1) / BPW : 1;
 
   uint16_t *const xl = (uint16_t *)smem;                               // XL: [rows][xp]
   const int xl_rows = XDT == SF_F32 ? 2 * B : B;
@@ -532,7 +534,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 constexpr int kBpwSet[6] = {1, 2, 4, 8, 11, 12};  // 11: K = 11008 (86 units) over 8 waves
 
 struct BlkPlan {
-  int T, BPW, nw, grid, nblk, ntiles, xl, xp, uq, ur;
+  int T, BPW, nw, grid, nblk, ntiles, xl, xp, uq, ur, kc;
   size_t lds;
 };
 
@@ -590,14 +592,16 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   p->nw = nw;
   p->uq = bpw;  // units per wave; the last wave takes what is left
   p->ur = 0;
-  const int wmax = max_waves(pre, (p->T == 1 && pre == PRE_RMSNORM && bpw <= 2 &&
-                                   p->ntiles > 256 * (16 / (nw < kMaxWaves ? nw : kMaxWaves)) ? 2 : p->T) * bpw);
-  if (nw > wmax) {
-    // K beyond what the waves hold at once: every wave loops over chunks of
-    // BPW units, the units split as evenly as the wave count allows
-    p->nw = nw = wmax;
+  p->kc = 0;
+  if (nw > max_waves(pre, p->T * bpw)) {
+    // K beyond what the waves hold at once: the plain GEMV's waves loop over
+    // chunks of BPW units, the units split as evenly as 16 waves allow (a
+    // folded producer or the RoPE epilogue is not built for it)
+    if (pre != PRE_NONE || rope || p->T != 1) return false;
+    p->nw = nw = kMaxWaves;
     p->uq = p->nblk / nw;
     p->ur = p->nblk % nw;
+    p->kc = 1;
   }
   // the folded RMSNorm's variants hold about 16 waves per CU: two row tiles
   // per workgroup when one would leave workgroups for a second round (T does
@@ -622,13 +626,13 @@ struct GemvArgs {
   const void *bias; int bdt; int B, N, K, G, g; bool asym; hipStream_t s;
 };
 
-template <int X, bool A, int GK, int T, int BPW, bool XL, int PRE, bool ROPE>
+template <int X, bool A, int GK, int T, int BPW, bool XL, int PRE, bool ROPE, bool KC = false>
 void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
                 const SfRopeAppend *rope, const int *pos_dev) {
   if (p.lds > 64 * 1024) {
     static bool attr = false;  // raise the dynamic LDS limit once per variant
     if (!attr) {
-      (void)hipFuncSetAttribute((const void *)k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE>,
+      (void)hipFuncSetAttribute((const void *)k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE, KC>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
       attr = true;
     }
@@ -637,7 +641,7 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
   const BlkArgs ba{g.w, g.st, g.zt, g.x, g.y, g.ydt, g.y32, g.bias, g.bdt, g.B, g.N, g.K, g.G, g.g,
                    p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps};
   const SfRopeAppend ra = rope ? *rope : SfRopeAppend{};
-  k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE><<<p.grid, p.nw * 64, p.lds, g.s>>>(ba, ra, pos_dev);
+  k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE, KC><<<p.grid, p.nw * 64, p.lds, g.s>>>(ba, ra, pos_dev);
 }
 
 // Runtime units-per-wave -> compiled variant. Compiled: T = 1 with every count
@@ -661,9 +665,23 @@ void by_bpw(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
 #undef SF_BPW
 }
 
+// The chunked plain GEMV (plan kc): T = 1 at the group kind's largest unit
+// count (a plan that needs chunks always takes it).
+template <int X, bool A, int GK>
+void launch_kc(const BlkPlan &p, const GemvArgs &g) {
+  constexpr int MB = max_bpw(GK, X != SF_F16);
+  if (p.BPW != MB) return;
+  if (p.xl) launch_cfg<X, A, GK, 1, MB, true, PRE_NONE, false, true>(p, g, nullptr, 0.f, nullptr, nullptr);
+  else if constexpr (X != SF_F32) launch_cfg<X, A, GK, 1, MB, false, PRE_NONE, false, true>(p, g, nullptr, 0.f, nullptr, nullptr);
+}
+
 template <int X, bool A, int GK>
 void by_mode(const BlkPlan &p, const GemvArgs &g, int pre, const float *pre_w, float eps,
              const SfRopeAppend *rope, const int *pos_dev) {
+  if (p.kc) {
+    launch_kc<X, A, GK>(p, g);
+    return;
+  }
   if (rope) {
     by_bpw<X, A, GK, 4, true, PRE_RMSNORM, true>(p, g, pre_w, eps, rope, pos_dev);
     return;
