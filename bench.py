@@ -340,7 +340,7 @@ def _config4(dev, lib, timer, cur, out, T):
                                  for _ in range(n - 1)]
     nsp = lib.sf_attn_default_splits_d(1, 2, T, 64)
     ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
-    wsp = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
+    wsp = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)  # split partials
     fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
                                                 a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
                                                 1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
@@ -349,7 +349,7 @@ def _config4(dev, lib, timer, cur, out, T):
     nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
     out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
                                  "bytes": nb, "splits": nsp,
-                                 "launches": "one (splits + fused merge)"}
+                                 "launches": "one" if nsp == 1 else "two (split partials, merge)"}
 
 
 def _kv_append(dev, lib, timer, cur, out):
@@ -648,11 +648,11 @@ def _short_kernel(name: str) -> str:
     import re
 
     m = (re.search(r"k_q4_gemv_blkILi(\d)ELb(\d)ELi(\d)ELi(\d)ELi(\d+)ELb(\d)ELi(\d)ELb(\d)E", name) or
-         re.search(r"k_q4_gemv_blk<(\d), (\w+), (\d), (\d), (\d+), (\w+), (\d), (\w+)>",
+         re.search(r"k_q4_gemv_blk<(\d), (\w+), (\d), (\d), (\d+), (\w+), (\d), (\w+)(?:, \w+)?>",
                    name.replace("true", "1").replace("false", "0")))
     if m:
         x = {"0": "f32", "1": "f16", "2": "bf16"}[m.group(1)]
-        pre = {"0": "", "1": ",pre=rmsnorm", "2": ",pre=silu"}[m.group(7)]
+        pre = {"0": "", "1": ",pre=rmsnorm", "2": ",pre=silu", "3": ",pre=attn-merge"}[m.group(7)]
         rope = ",rope+append" if m.group(8) == "1" else ""
         src = "lds" if m.group(6) == "1" else "direct"
         return (f"k_q4_gemv_blk<x={x},asym={m.group(2)},gk={m.group(3)},T={m.group(4)},"

@@ -175,17 +175,19 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
  * 200-261). q: [B, H, D] of q_dtype; out: [B, H, D] of out_dtype. n_splits is
  * the split-T count (the reference's n_tiles; <=0 picks a default; at most
  * 512). D <= 256 (the reference's bound, q4_attention.py:78,227-228) and
- * D % 8 == 0. One launch: the splits' partials are merged by the last split
- * to finish.
+ * D % 8 == 0. One split is one launch; more splits write their partials
+ * (m, l, acc) to the workspace and a second launch merges them with the
+ * reference's combine rule (q4_attention.py:63-70, 256-261), the splits in
+ * order.
  * workspace: sf_attn_workspace_bytes(B, H, D, n_splits) bytes, 256-byte
- * aligned, ZERO-FILLED before its first use. Its first 16 KiB hold merge
- * counters that every call leaves at zero, so one workspace serves later
- * calls of any shape. Calls that share a workspace must not overlap (use one
- * workspace per stream). */
+ * aligned (NULL for one split), no initial contents needed: acc
+ * [B*H][n_splits][D] fp32 at offset 0, then (m, l) [B*H][n_splits][2] fp32
+ * at the next 256-byte boundary. Calls that share a workspace must not
+ * overlap (use one workspace per stream). */
 size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
 /* Default split count (the reference's _choose_n_tiles, q4_attention.py:183-197,
- * re-tuned for MI355X): one split up to 1280 cached tokens at head_dim <= 64
- * and up to 640 above, then about 128 tokens per split, at most 64.
+ * re-tuned for MI355X): one split up to 896 cached tokens at head_dim <= 64
+ * and up to 448 above, then about 128 tokens per split, 16 to 64 splits.
  * sf_attn_default_splits is the head_dim-64 rule. */
 int sf_attn_default_splits(int B, int KVH, int T);
 int sf_attn_default_splits_d(int B, int KVH, int T, int D);
@@ -198,7 +200,7 @@ int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const
 /* No counterpart in the reference: sf_attn_decode_i8kv for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Same arguments and result, without the workspace: the
- * split partials and merge counters live in a fixed device array of
+ * split partials live in a fixed device array of
  * sf_attn_noalloc_max_bytes() (4 MiB) per GPU, held until the process ends;
  * shapes whose workspace would exceed it (sf_attn_workspace_bytes) return
  * SF_EINVAL. The call allocates nothing. Calls that overlap on one GPU (two
@@ -220,6 +222,35 @@ int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
                             int T_add, int T_max, int T_cap, int D, float scale, int n_splits,
                             void *stream);
 
+/* sf_attn_decode_i8kv_dev without the merge launch, for a consumer that merges
+ * the split partials itself (sf_q4_gemv_attn_merge, the decoder's o
+ * projection): leaves the partials of n_splits (2..512) splits in the
+ * workspace in the layout above and writes no output. No counterpart in the
+ * reference (its decode kernel merges in the same dispatch,
+ * q4_attention.py:256-261). */
+int sf_attn_decode_i8kv_partials_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                                     const void *k_scales, const int8_t *v_codes,
+                                     const void *v_scales, int scale_dtype, void *workspace,
+                                     size_t workspace_bytes, int B, int H, int KVH,
+                                     const int *T_dev, int T_add, int T_max, int T_cap, int D,
+                                     float scale, int n_splits, void *stream);
+
+/* The decoder's o projection with the attention's split merge folded into its
+ * activation load: x[b, h*D + d] is the merged attention output of the split
+ * partials in `workspace` (sf_attn_decode_i8kv_partials_dev, B rows of H heads,
+ * n_splits = 2..8), rounded to act_dtype, and y = W x as sf_q4_gemv (K = H*D).
+ * Bit-identical to sf_attn_decode_i8kv writing an act_dtype output followed by
+ * sf_q4_gemv on it. sf_q4_gemv_attn_merge_supported says which shapes (1);
+ * others return SF_EUNSUPPORTED. No counterpart in the reference, which runs
+ * the attention and Q4Linear o_proj as separate ops
+ * (/root/reference/siliconfer/model/layers.py:120-133). */
+int sf_q4_gemv_attn_merge_supported(int B, int N, int H, int D, int n_splits, int group_size,
+                                    int act_dtype);
+int sf_q4_gemv_attn_merge(const void *blob, const void *workspace, size_t workspace_bytes,
+                          int n_splits, int H, int D, int act_dtype, void *y, int y_dtype,
+                          float *y_f32, const void *bias, int bias_dtype, int B, int N,
+                          int group_size, int has_zeros, void *stream);
+
 /* Causal prefill attention over a batch-1 int8 cache: query row i of q
  * [T_q][H][D] attends to the first T0 + i + 1 cached tokens (the prompt's own
  * keys already appended). Replaces the reference's prompt path, which
@@ -234,8 +265,8 @@ int sf_attn_prefill_i8kv(const void *q, int q_dtype, const int8_t *k_codes, cons
  * kernel runs): the verify rows of speculative decoding replayed from a HIP
  * graph at a position the host does not know when it records the launch.
  * n_splits (<= 0: sf_attn_default_splits_d(T_q, KVH, T_max, D)) and the workspace
- * (sf_attn_workspace_bytes(T_q, H, D, n_splits), zero-filled before its first
- * use) are fixed for T0 + T_q <= T_max; rows past T_cap see T_cap tokens. */
+ * (sf_attn_workspace_bytes(T_q, H, D, n_splits)) are fixed for T0 + T_q <= T_max;
+ * rows past T_cap see T_cap tokens. */
 int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,
                              const void *k_scales, const int8_t *v_codes, const void *v_scales,
                              int scale_dtype, void *out, int out_dtype, void *workspace,

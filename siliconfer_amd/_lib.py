@@ -62,6 +62,12 @@ _SIGS = {
     "sf_attn_decode_i8kv_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                        _c_p, _c_sz, _c_i, _c_i, _c_i, _c_p, _c_i, _c_i, _c_i,
                                        _c_i, _c_f, _c_i, _c_p]),
+    "sf_attn_decode_i8kv_partials_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_sz,
+                                                _c_i, _c_i, _c_i, _c_p, _c_i, _c_i, _c_i, _c_i, _c_f,
+                                                _c_i, _c_p]),
+    "sf_q4_gemv_attn_merge_supported": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
+    "sf_q4_gemv_attn_merge": (_c_i, [_c_p, _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_p, _c_i, _c_p, _c_p,
+                                     _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_attn_prefill_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                     _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_p]),
     "sf_attn_prefill_i8kv_dev": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p,

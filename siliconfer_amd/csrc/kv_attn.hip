@@ -19,16 +19,18 @@
 //    the block in registers; each lane keeps its own online softmax (in base
 //    2, scores pre-scaled by log2 e) over its tokens, loading K and V codes
 //    with 8-byte loads a batch ahead; the lane states are merged through LDS;
-//  * the split partials (m, l, acc[D]) go to a workspace; the last workgroup
-//    of each (b, kv head, head block) to finish merges them in the same
-//    launch with the reference's combine rule (q4_attention.py:63-70,
-//    256-261); a single split writes the output directly.
+//  * the split partials (m, l, acc[D]) go to a workspace and a second,
+//    small launch merges them with the reference's combine rule
+//    (q4_attention.py:63-70, 256-261; split_merge.h), one lane per output
+//    element; the decoder instead folds that merge into its o-projection
+//    GEMV (sf_q4_gemv_attn_merge). A single split writes the output directly.
 #include <math.h>
 #include <stdlib.h>
 
 #include <mutex>
 
 #include "sf_common.h"
+#include "split_merge.h"
 
 namespace {
 
@@ -88,13 +90,12 @@ k_kv_quant_append(const void *__restrict__ k_new, const void *__restrict__ v_new
 }
 
 // ---------------------------------------------------------------------------
-// split-T decode attention, combine fused into the same launch
+// split-T decode attention
 // ---------------------------------------------------------------------------
 constexpr int kMaxD = 256;
 constexpr int kMaxSplits = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kAttnBatch = 4;  // rows per lane per load batch
-constexpr int kMergeChunk = 32;  // partials per thread loaded at once by the merge
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -144,164 +145,11 @@ __device__ __forceinline__ void i8x8_to_f32(u32x2 c, float (&f)[8]) {
   }
 }
 
-// Data handed between workgroups (split partials, merge counters) moves with
-// agent-scope relaxed atomics: they are coherent across the XCDs' L2 caches
-// by themselves, without the whole-L2 write-back / invalidate that an
-// agent-scope release / acquire fence costs. Order comes from completion:
-// the partial stores are waited for (vmcnt 0) before the counter increment,
-// and the merge's loads are issued only after the increment has returned.
-__device__ __forceinline__ void st_agent(float *p, float v) {
-  __hip_atomic_store((uint32_t *)p, sf_bitcast<uint32_t>(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2_t ld2_agent(const float *p) {
-  return sf_bitcast<float2_t>(
-      __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
 template <int HB>
 constexpr int attn_smem_floats() {
-  // main phase: acc [NS][HB][D] (NS * D <= 2048 per head), m and l [NS][HB]
-  // (NS <= 256), M and L [HB]; merge phase: slice sums [NT] float4, split
-  // weights and l [HB][kMaxSplits] each, L [HB]
-  constexpr int a = 2048 * HB + 2 * 256 * HB + 2 * HB;
-  constexpr int b = 4 * kAttnThreads + 2 * HB * kMaxSplits + HB;
-  return a > b ? a : b;
-}
-
-// Cross-split merge of a split-T launch, called by every workgroup after it
-// has stored its partial (m, l, acc[D] per head) with agent-scope stores: the
-// last workgroup of the (b, kv head, head block) group to arrive (counter
-// `ctr`) merges all splits' partials with the reference's combine rule
-// (q4_attention.py:63-70, 256-261), writes the output rows bh0 .. bh0+nh-1
-// and resets the counter. smem holds at least 4 * kAttnThreads + 2 * HB *
-// MAXS + HB floats.
-template <int HB, int MAXS>
-__device__ __forceinline__ void attn_merge_splits(float *smem, int *s_last, const float *part_acc,
-                                                  const float *part_ml, unsigned *ctr, size_t bh0,
-                                                  int nh, int D, int n_splits, void *out, int odt) {
-  constexpr int NT = kAttnThreads;
-  const int tid = threadIdx.x;
-  const int nq = D >> 2;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_last = prev == (unsigned)(n_splits - 1);
-  }
-  __syncthreads();
-  if (!*s_last) return;
-
-  // Partials of (head, 4-dim quad) items; with fewer items than threads the
-  // splits are cut into nsl slices whose sums are folded through LDS. Each
-  // thread's first kMergeChunk partials are loaded before the (m, l) staging
-  // so that all loads of the merge are in flight together.
-  float4_t *red4 = (float4_t *)smem;        // [NT]
-  float *cw = smem + 4 * NT;                // [HB][MAXS]: m, then weights
-  float *cl = cw + HB * MAXS;         // [HB][MAXS]: l
-  float *Lg = cl + HB * MAXS;         // [HB]
-  const int items = nh * nq;
-  const int nsl = items >= NT ? 1 : NT / items;
-  const int units = items * nsl;            // (item, slice) pairs
-  auto part4 = [&](int item, int s) {
-    const int h = item / nq, dqq = (item - h * nq) * 4;
-    const float *pp = part_acc + ((bh0 + h) * n_splits + s) * D + dqq;
-    const float2_t lo = ld2_agent(pp), hi = ld2_agent(pp + 2);
-    return float4_t{lo.x, lo.y, hi.x, hi.y};
-  };
-  constexpr int CH = kMergeChunk;
-  float4_t pre[CH];
-  {
-    const int unit = tid < units ? tid : 0;
-    const int item = unit % items, sl = unit / items;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) pre[j] = part4(item, min(sl + j * nsl, n_splits - 1));
-  }
-  // split weights: 32 lanes per head, lane j covering splits j, j + 32, ...;
-  // heads h0 + tid / 32 for h0 = 0, 8, ... (every thread takes the same number
-  // of rounds, so the 32-lane reductions always see whole groups)
-  for (int h0 = 0; h0 < HB; h0 += NT / 32) {
-    const int h = h0 + (tid >> 5), j = tid & 31;
-    const bool on = h < nh;
-    const float *mlh = part_ml + (bh0 + (on ? h : 0)) * n_splits * 2;
-    // the first two are loaded unconditionally (clamped) to keep them in flight together
-    const float2_t ml0 = ld2_agent(mlh + 2 * min(j, n_splits - 1));
-    const float2_t ml1 = ld2_agent(mlh + 2 * min(j + 32, n_splits - 1));
-    float mx = -INFINITY;
-    if (on) {
-      if (j < n_splits) {
-        cw[h * MAXS + j] = ml0.x;
-        cl[h * MAXS + j] = ml0.y;
-        mx = ml0.x;
-      }
-      if (j + 32 < n_splits) {
-        cw[h * MAXS + j + 32] = ml1.x;
-        cl[h * MAXS + j + 32] = ml1.y;
-        mx = fmaxf(mx, ml1.x);
-      }
-      for (int s = j + 64; s < n_splits; s += 32) {
-        const float2_t ml = ld2_agent(mlh + 2 * s);
-        cw[h * MAXS + s] = ml.x;
-        cl[h * MAXS + s] = ml.y;
-        mx = fmaxf(mx, ml.x);
-      }
-    }
-    const float M = group32_max(mx);
-    const float M_ref = M == -INFINITY ? 0.f : M;
-    float lsum = 0.f;
-    if (on)
-      for (int s = j; s < n_splits; s += 32) {
-        const float w = __builtin_amdgcn_exp2f(cw[h * MAXS + s] - M_ref);
-        cw[h * MAXS + s] = w;
-        lsum = fmaf(cl[h * MAXS + s], w, lsum);
-      }
-    lsum = group32_sum(lsum);
-    if (on && j == 0) Lg[h] = lsum;
-  }
-  __syncthreads();
-  auto unit_sum = [&](int unit, bool first) {
-    const int item = unit % items, sl = unit / items, h = item / nq;
-    const float *w = cw + h * MAXS;
-    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-    int j0 = 0;
-    if (first) {
-#pragma unroll
-      for (int j = 0; j < CH; j += 2) {
-        const int s0 = sl + j * nsl, s1 = s0 + nsl;
-        a0 += pre[j] * (s0 < n_splits ? w[s0] : 0.f);
-        a1 += pre[j + 1] * (s1 < n_splits ? w[s1] : 0.f);
-      }
-      j0 = CH;
-    }
-    for (int s = sl + j0 * nsl; s < n_splits; s += nsl) a0 += part4(item, s) * w[s];
-    return a0 + a1;
-  };
-  auto write_item = [&](int item, float4_t a) {
-    const int h = item / nq, dqq = (item - h * nq) * 4;
-    const float L = Lg[h];
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const size_t o = (bh0 + h) * D + dqq;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = a[i] * inv;
-      if (odt == SF_F32) ((float *)out)[o + i] = v;
-      else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
-      else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
-    }
-  };
-  if (nsl == 1) {
-    for (int item = tid; item < items; item += NT) write_item(item, unit_sum(item, item == tid));
-  } else {
-    if (tid < units) red4[tid] = unit_sum(tid, true);
-    __syncthreads();
-    if (tid < items) {
-      float4_t a = red4[tid];
-      for (int k = 1; k < nsl; ++k) a += red4[k * items + tid];
-      write_item(tid, a);
-    }
-  }
-  if (tid == 0)  // ready for the next call on this workspace
-    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // acc [NS][HB][D] (NS * D <= 2048 per head), m and l [NS][HB] (NS <= 256),
+  // M and L [HB]
+  return 2048 * HB + 2 * 256 * HB + 2 * HB;
 }
 
 // One workgroup per (split, kv head, block of HB query heads, batch row); the
@@ -314,19 +162,16 @@ __device__ __forceinline__ void attn_merge_splits(float *smem, int *s_last, cons
 // its own online-softmax state per head (m, l, acc[8]) with no block-level
 // synchronisation. At the end the NS = 4 * 64 / OCT lane states of each head
 // are merged through LDS into the split's partial; with one split it is the
-// output, otherwise the last workgroup of the (b, kv head, head block) group
-// to finish (device-scope counter) merges all splits' partials with the
-// reference's rule, writes the output and resets the counter.
+// output, otherwise the partial of the split (merged by a later launch).
 template <int QDT, int SDT, int HB>
 __global__ void __launch_bounds__(kAttnThreads)
 k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
               const void *__restrict__ ks, const int8_t *__restrict__ vc,
-              const void *__restrict__ vs, float *part_acc, float *part_ml, unsigned *counters,
+              const void *__restrict__ vs, float *part_acc, float *part_ml,
               void *__restrict__ out, int odt, int H, int KVH, int T, const int *__restrict__ T_dev,
               int causal, int T_cap, int D, float qscale, int n_splits, int oct_log2) {
   constexpr int NT = kAttnThreads, NW = kAttnWaves, U = kAttnBatch;
   __shared__ __attribute__((aligned(16))) float smem[attn_smem_floats<HB>()];
-  __shared__ int s_last;
 
   const int OCT = 1 << oct_log2;  // lanes per token
   const int R = 64 >> oct_log2;   // tokens per row
@@ -529,20 +374,11 @@ k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
         else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
       }
     } else {
-      float *pa = part_acc + ((bh0 + h) * n_splits + split) * D + dq4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st_agent(pa + i, a[i]);
+      *(float4_t *)(part_acc + ((bh0 + h) * n_splits + split) * D + dq4) = a;
     }
   }
-  if (single) return;
-  if (tid < nh) {
-    st_agent(part_ml + ((bh0 + tid) * n_splits + split) * 2 + 0, Ms[tid]);
-    st_agent(part_ml + ((bh0 + tid) * n_splits + split) * 2 + 1, Ls[tid]);
-  }
-
-  attn_merge_splits<HB, kMaxSplits>(smem, &s_last, part_acc, part_ml,
-                                     counters + ((size_t)b * KVH + kvh) * n_hblk + hblk, bh0, nh, D,
-                                     n_splits, out, odt);
+  if (!single && tid < nh)
+    *(float2_t *)(part_ml + ((bh0 + tid) * n_splits + split) * 2) = float2_t{Ms[tid], Ls[tid]};
 }
 
 // ---------------------------------------------------------------------------
@@ -568,8 +404,8 @@ k_attn_decode(const void *__restrict__ q, const int8_t *__restrict__ kc,
 //    address and lane 8 + i byte i of the odd lanes' rows, so lane 2s + h of
 //    group g addresses token T_g[s], dims 16 db + 8 h .. + 7.
 // The next tile's loads are issued before the current tile's math. At the
-// end the 4 wave states are merged through LDS into the split's partial (or
-// the output), then attn_merge_splits combines the splits.
+// end the wave states are merged through LDS into the split's partial (or
+// the output).
 constexpr int kMfmaMaxSplits = 128;
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -588,15 +424,12 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint32_t lo, uint32_t hi) {
 
 template <int D, int NW>
 constexpr int attn_mfma_smem_floats() {
-  // main phase: V tiles [NW][32][D + 8] bytes, then wave states m, l [NW][16]
-  // and O [NW][16][D]; merge phase (4 waves only): attn_merge_splits<16, kMfmaMaxSplits>
-  constexpr int a = NW * 32 * (D + 8) / 4 + 2 * NW * 16 + NW * 16 * D;
-  constexpr int b = NW == kAttnWaves ? 4 * kAttnThreads + 2 * 16 * kMfmaMaxSplits + 16 : 0;
-  return a > b ? a : b;
+  // V tiles [NW][32][D + 8] bytes, then wave states m, l [NW][16] and O [NW][16][D]
+  return NW * 32 * (D + 8) / 4 + 2 * NW * 16 + NW * 16 * D;
 }
 
 // NW waves per workgroup, NB of a wave's tiles in flight. NW = 4 serves
-// split-T launches (the cross-split merge runs on 256 threads); one split per
+// split-T launches; one split per
 // (b, kv head) runs 16 waves with one tile each in flight at head_dim 64 (more
 // tiles per wave spill at 128 VGPRs) and 8 waves with 2 at head_dim 128, so a
 // 512-token cache is one round of loads and needs no cross-workgroup merge.
@@ -606,7 +439,7 @@ template <int QDT, int SDT, int D, int NW, int NB>
 __global__ void __launch_bounds__(NW * 64)
 k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
             const int8_t *__restrict__ vc, const void *__restrict__ vs, float *part_acc,
-            float *part_ml, unsigned *counters, void *__restrict__ out, int odt, int H, int KVH,
+            float *part_ml, void *__restrict__ out, int odt, int H, int KVH,
             int T, const int *__restrict__ T_dev, int causal, int T_cap, float qscale,
             int n_splits, int vscale) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
@@ -619,7 +452,6 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   constexpr int PITCH = D + 8;     // V tile row pitch in LDS, bytes
   constexpr bool QSPLIT = QDT != SF_F16;
   __shared__ __attribute__((aligned(16))) float smem[attn_mfma_smem_floats<D, NW>()];
-  __shared__ int s_last;
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = H / KVH;
@@ -836,20 +668,9 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
         else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
       }
     } else {
-      float *pa = part_acc + ((bh0 + h) * n_splits + split) * D + d4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st_agent(pa + i, a[i]);
-      if (d4 == 0) {
-        st_agent(part_ml + ((bh0 + h) * n_splits + split) * 2 + 0, M);
-        st_agent(part_ml + ((bh0 + h) * n_splits + split) * 2 + 1, L);
-      }
+      *(float4_t *)(part_acc + ((bh0 + h) * n_splits + split) * D + d4) = a;
+      if (d4 == 0) *(float2_t *)(part_ml + ((bh0 + h) * n_splits + split) * 2) = float2_t{M, L};
     }
-  }
-  if constexpr (NW == kAttnWaves) {
-    if (single) return;
-    attn_merge_splits<16, kMfmaMaxSplits>(smem, &s_last, part_acc, part_ml,
-                                          counters + (size_t)b * KVH + kvh, bh0, G, D, n_splits,
-                                          out, odt);
   }
 }
 
@@ -1116,42 +937,88 @@ extern "C" int sf_kv_quant_append(const void *k_new, const void *v_new, int in_d
   return sf_check_launch("sf_kv_quant_append");
 }
 
-// Workspace: a fixed 16 KiB region of uint32 counters (one per (b, kv head,
-// head block) of a call), then partial acc [B*H][S][D] fp32, then (m, l)
-// [B*H][S][2]. The counters sit at the same place for every shape, so one
-// zero-filled workspace serves calls of any shape: each call's last split
-// resets the counter it used.
-constexpr size_t kCounterBytes = 16384;
-constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(unsigned));
+namespace {
 
-static size_t attn_ws_parts(int B, int H, int D, int S, size_t *acc_off, size_t *ml_off) {
-  const size_t rows = (size_t)B * H * S;
-  *acc_off = kCounterBytes;
-  *ml_off = sf_align256(*acc_off + rows * D * sizeof(float));
-  return *ml_off + rows * 2 * sizeof(float);
+// Merge launch of a split-T call: one lane per output element (row bh, dim d),
+// the splits in order with the rule of split_merge.h. Up to kMergeLoadSplits
+// splits, every load of the element goes out before the first use; longer
+// rows take M in a first pass.
+constexpr int kMergeLoadSplits = 64;
+constexpr int kMergeThreads = 64;
+
+__global__ void __launch_bounds__(kMergeThreads)
+k_attn_merge(const float *__restrict__ acc, const float *__restrict__ ml, void *__restrict__ out,
+             int odt, int rows, int D, int S) {
+  constexpr int C = kMergeLoadSplits;
+  const int e = blockIdx.x * kMergeThreads + threadIdx.x;
+  if (e >= rows * D) return;
+  const int bh = e / D, d = e - bh * D;
+  const float2_t *mlr = (const float2_t *)ml + (size_t)bh * S;
+  const float *ar = acc + (size_t)bh * S * D + d;
+  float L = 0.f, v = 0.f;
+  if (S <= C) {
+    float2_t mv[C];
+    float av[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+      if (j < S) {
+        mv[j] = mlr[j];
+        av[j] = ar[(size_t)j * D];
+      }
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+      if (j < S) M = fmaxf(M, mv[j].x);
+    const float mref = sf_merge_mref(M);
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+      if (j < S) {
+        const float w = sf_merge_weight(mv[j].x, mref);
+        L = fmaf(mv[j].y, w, L);
+        v = fmaf(av[j], w, v);
+      }
+  } else {
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, mlr[s].x);
+    const float mref = sf_merge_mref(M);
+    for (int s = 0; s < S; ++s) {
+      const float2_t p = mlr[s];
+      const float w = sf_merge_weight(p.x, mref);
+      L = fmaf(p.y, w, L);
+      v = fmaf(ar[(size_t)s * D], w, v);
+    }
+  }
+  const float r = sf_merge_finish(L, v);
+  if (odt == SF_F32) ((float *)out)[e] = r;
+  else if (odt == SF_F16) ((f16 *)out)[e] = (f16)r;
+  else ((uint16_t *)out)[e] = sf_f32_to_bf16(r);
 }
 
+}  // namespace
+
+// Workspace: the split partials of split_merge.h, acc [B*H][S][D] fp32 then
+// (m, l) [B*H][S][2]. Nothing in it needs clearing: every split writes its
+// partial before the merge reads it.
 extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
   if (B <= 0 || H <= 0 || D <= 0 || n_splits <= 0) return 0;
   if (n_splits > kMaxSplits) n_splits = kMaxSplits;
   size_t acc_off, ml_off;
-  return attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
+  return sf_split_ws_parts(B * H, D, n_splits, &acc_off, &ml_off);
 }
 
 extern "C" int sf_attn_default_splits_d(int B, int KVH, int T, int D) {
-  // One split (one workgroup per kv head, no cross-workgroup merge) up to
-  // 1280 tokens at head_dim 64 and 640 at larger head dims: measured on MI355X
-  // at 14 / 2 heads against the split launch (head_dim 64: 9.4 against 9.9 us
-  // at 1280, 10.6 against 9.7 at 1536; head_dim 128: 10.4 against 11.0 at 640,
-  // 11.4 against 11.0 at 768). Beyond: about 128 tokens per split, at most 64
-  // splits so that the final merge's loads of the partials all go out at once
-  // (32 splits for T = 4096 and 64 for T = 16384 are the fastest of 1..128).
+  // One split (one workgroup per kv head, no merge launch) up to 896 tokens at
+  // head_dim 64 and 448 at larger head dims; beyond, about 128 tokens per
+  // split, at least 16 and at most 64 splits. Measured on MI355X at 14 / 2
+  // heads, head_dim 64 (us, one split / best split count): T = 512: 6.6 / 7.9;
+  // 1024: 8.7 / 8.2 (16-32 splits); 4096: 22.5 / 8.9 (32); 16384: 79.5 / 11.0 (64).
   (void)B;
   (void)KVH;
-  if (T <= (D <= 64 ? 1280 : 640)) return 1;
+  if (T <= (D <= 64 ? 896 : 448)) return 1;
   int s = (T + 127) / 128;
+  if (s < 16) s = 16;
   if (s > 64) s = 64;
-  return s < 1 ? 1 : s;
+  return s;
 }
 
 extern "C" int sf_attn_default_splits(int B, int KVH, int T) {
@@ -1164,11 +1031,27 @@ static int attn_heads_per_block(int G) {
 
 // Shared checks and launch. T_dev: device length (plus T); causal: prefill
 // rows, query row b sees T + b + 1 tokens of a batch-1 cache.
+// The merge launch after a split attention launch (none for one split, or
+// when the caller merges the partials itself).
+static int attn_merge_launch(const char *what, const float *part_acc, const float *part_ml,
+                             void *out, int odt, int rows, int D, int n_splits, hipStream_t st,
+                             int merge) {
+  if (n_splits > 1 && merge) {
+    const int n = rows * D;
+    k_attn_merge<<<(n + kMergeThreads - 1) / kMergeThreads, kMergeThreads, 0, st>>>(
+        part_acc, part_ml, out, odt, rows, D, n_splits);
+  }
+  return sf_check_launch(what);
+}
+
+// merge = 0 leaves a split launch's partials in the workspace for a consumer
+// that merges them itself (sf_q4_gemv_attn_merge).
 static int attn_launch(const char *what, const void *q, int q_dtype, const int8_t *k_codes,
                        const void *k_scales, const int8_t *v_codes, const void *v_scales,
                        int scale_dtype, void *out, int out_dtype, void *workspace,
                        size_t workspace_bytes, int B, int H, int KVH, int T, const int *T_dev,
-                       int causal, int T_cap, int D, float scale, int n_splits, void *stream) {
+                       int causal, int T_cap, int D, float scale, int n_splits, void *stream,
+                       int merge = 1) {
   SF_REQUIRE(H % KVH == 0, SF_EINVAL, "n_heads=%d not a multiple of n_kv_heads=%d", H, KVH);
   SF_REQUIRE(D <= kMaxD, SF_EINVAL, "head_dim=%d exceeds kernel's compile-time max 256", D);
   SF_REQUIRE(D % 8 == 0, SF_EUNSUPPORTED, "head_dim=%d: need a multiple of 8", D);
@@ -1185,17 +1068,15 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
   if (n_splits < 1) n_splits = 1;
   size_t acc_off = 0, ml_off = 0;
   float *part_acc = nullptr, *part_ml = nullptr;
-  unsigned *counters = nullptr;
   if (n_splits > 1) {
     SF_REQUIRE(workspace, SF_EINVAL, "null workspace");
     SF_REQUIRE(((uintptr_t)workspace & 255) == 0, SF_EINVAL, "workspace must be 256-byte aligned");
     const size_t need = sf_attn_workspace_bytes(B, H, D, n_splits);
     SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "attention workspace too small: %zu < %zu",
                workspace_bytes, need);
-    attn_ws_parts(B, H, D, n_splits, &acc_off, &ml_off);
+    sf_split_ws_parts(B * H, D, n_splits, &acc_off, &ml_off);
     part_acc = (float *)((char *)workspace + acc_off);
     part_ml = (float *)((char *)workspace + ml_off);
-    counters = (unsigned *)workspace;
   }
   const int G = H / KVH;
   const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
@@ -1206,9 +1087,6 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
   const bool mfma_ok = !(mfma_env && mfma_env[0] == '0');
   if (mfma_ok && G <= 16 && (D == 64 || D == 128) && n_splits <= kMfmaMaxSplits &&
       (((uintptr_t)k_codes | (uintptr_t)v_codes) & 15) == 0) {
-    SF_REQUIRE(n_splits == 1 || B * KVH <= kMaxCounters, SF_EUNSUPPORTED,
-               "attention batch too large for one call (B * n_kv_heads = %d > %d)", B * KVH,
-               kMaxCounters);
     dim3 grid(n_splits, KVH, B);
     // scale loads in aligned groups of 4 tokens when every row start allows it
     const size_t sal = scale_dtype == SF_F16 ? 8 : 16;
@@ -1216,7 +1094,7 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
                        (uintptr_t)v_scales % sal == 0;
 #define SF_MFMA_LAUNCH(QD, SD, DD, NWV, NBV)                                                     \
   k_attn_mfma<QD, SD, DD, NWV, NBV><<<grid, NWV * 64, 0, st>>>(                                  \
-      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H,   \
+      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, out, out_dtype, H,   \
       KVH, T, T_dev, causal, T_cap, qscale, n_splits, vscale)
 #define SF_MFMA_D(QD, SD)                                   \
   do {                                                      \
@@ -1239,18 +1117,15 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
     }
 #undef SF_MFMA_D
 #undef SF_MFMA_LAUNCH
-    return sf_check_launch(what);
+    return attn_merge_launch(what, part_acc, part_ml, out, out_dtype, B * H, D, n_splits, st, merge);
   }
   const int HB = attn_heads_per_block(G);
   const int n_hblk = (G + HB - 1) / HB;
-  SF_REQUIRE(n_splits == 1 || B * KVH * n_hblk <= kMaxCounters, SF_EUNSUPPORTED,
-             "attention batch too large for one call (B * n_kv_heads * head blocks = %d > %d)",
-             B * KVH * n_hblk, kMaxCounters);
   const int oct_log2 = pow2_log2_at_least(D / 8);
   dim3 grid(n_splits, KVH * n_hblk, B);
 #define SF_ATTN_LAUNCH(QD, SD, HBV)                                                            \
   k_attn_decode<QD, SD, HBV><<<grid, kAttnThreads, 0, st>>>(                                   \
-      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, counters, out, out_dtype, H, \
+      q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, out, out_dtype, H, \
       KVH, T, T_dev, causal, T_cap, D, qscale, n_splits, oct_log2)
 #define SF_ATTN_HB(QD, SD)                       \
   do {                                           \
@@ -1272,7 +1147,7 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
   }
 #undef SF_ATTN_HB
 #undef SF_ATTN_LAUNCH
-  return sf_check_launch(what);
+  return attn_merge_launch(what, part_acc, part_ml, out, out_dtype, B * H, D, n_splits, st, merge);
 }
 
 extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes,
@@ -1306,6 +1181,25 @@ extern "C" int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t 
   return attn_launch("sf_attn_decode_i8kv_dev", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, B, H, KVH, T_add,
                      T_dev, 0, T_cap, D, scale, n_splits, stream);
+}
+
+extern "C" int sf_attn_decode_i8kv_partials_dev(const void *q, int q_dtype, const int8_t *k_codes,
+                                                const void *k_scales, const int8_t *v_codes,
+                                                const void *v_scales, int scale_dtype,
+                                                void *workspace, size_t workspace_bytes, int B,
+                                                int H, int KVH, const int *T_dev, int T_add,
+                                                int T_max, int T_cap, int D, float scale,
+                                                int n_splits, void *stream) {
+  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T_max >= 0 && T_max <= T_cap, SF_EINVAL,
+             "invalid attention shape B=%d H=%d KVH=%d T_max=%d T_cap=%d D=%d", B, H, KVH, T_max,
+             T_cap, D);
+  SF_REQUIRE(T_dev, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(n_splits >= 2 && n_splits <= kMaxSplits, SF_EINVAL,
+             "partials need 2..%d splits (got %d)", kMaxSplits, n_splits);
+  // `out` is never written by a split launch: the workspace stands in for it
+  return attn_launch("sf_attn_decode_i8kv_partials_dev", q, q_dtype, k_codes, k_scales, v_codes,
+                     v_scales, scale_dtype, workspace, SF_F32, workspace, workspace_bytes, B, H,
+                     KVH, T_add, T_dev, 0, T_cap, D, scale, n_splits, stream, 0);
 }
 
 // Flash-style prefill (k_attn_prefill_mfma) for prompt chunks of kPfMinRows
@@ -1406,32 +1300,26 @@ extern "C" int sf_attn_prefill_i8kv_dev(const void *q, int q_dtype, const int8_t
 
 // ---------------------------------------------------------------------------
 // Decode attention that allocates nothing: sf_attn_decode_i8kv with its
-// workspace (split partials and merge counters) in a file-scope device array.
-// Each GPU the library runs on holds its own copy until the process ends;
-// host code reaches a device's copy only through the address
-// hipGetSymbolAddress gives for it (taken once per device, on the first call,
-// with that device current), never through the array's name. The first call
-// on a device also zeroes the counters with a fill kernel on the caller's
-// stream; every call leaves them at zero again (the merging split resets the
-// counter it used). All calls on one GPU share the array: calls that overlap
-// on one GPU (two streams at once) race.
+// workspace (the split partials) in a file-scope device array. Each GPU the
+// library runs on holds its own copy until the process ends; host code
+// reaches a device's copy only through the address hipGetSymbolAddress gives
+// for it (taken once per device, on the first call, with that device
+// current), never through the array's name. Nothing in it needs clearing
+// (every split writes its partial before the merge launch reads it). All
+// calls on one GPU share the array: calls that overlap on one GPU (two
+// streams at once) race.
 // ---------------------------------------------------------------------------
 constexpr size_t kNoAllocScratchBytes = 4u << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace {
 
-__global__ void k_zero_words(uint32_t *p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices];
 
 // the current device's copy of `scratch`, set up on its first use
-int scratch_for_current_device(hipStream_t stream, void **out) {
+int scratch_for_current_device(void **out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   SF_REQUIRE(e == hipSuccess, SF_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
@@ -1443,10 +1331,6 @@ int scratch_for_current_device(hipStream_t stream, void **out) {
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     SF_REQUIRE(e == hipSuccess && p, SF_EHIP, "hipGetSymbolAddress(scratch): %s",
                hipGetErrorString(e));
-    const int words = (int)(kCounterBytes / sizeof(uint32_t));
-    k_zero_words<<<(words + 255) / 256, 256, 0, stream>>>((uint32_t *)p, words);
-    int rc = sf_check_launch("sf_attn_decode_i8kv_noalloc: zeroing the counters");
-    if (rc) return rc;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -1472,7 +1356,7 @@ extern "C" int sf_attn_decode_i8kv_noalloc(const void *q, int q_dtype, const int
              "scratch, more than its fixed %zu; use sf_attn_decode_i8kv with a workspace",
              B, H, D, s, need, kNoAllocScratchBytes);
   void *ws = nullptr;
-  int rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  int rc = scratch_for_current_device(&ws);
   if (rc) return rc;
   return sf_attn_decode_i8kv(q, q_dtype, k_codes, k_scales, v_codes, v_scales, scale_dtype, out,
                              out_dtype, ws, kNoAllocScratchBytes, B, H, KVH, T, T_cap, D, scale, s,

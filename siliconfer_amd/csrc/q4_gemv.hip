@@ -153,6 +153,49 @@ extern "C" int sf_q4_gemv_fused(const void *blob, const float *src, int op, cons
                                bias_dtype, 1, N, K, group_size, has_zeros, stream);
 }
 
+extern "C" int sf_q4_gemv_attn_merge_supported(int B, int N, int H, int D, int n_splits,
+                                               int group_size, int act_dtype) {
+  if (B < 1 || B > 8 || N <= 0 || H <= 0 || D <= 0 || D % 8 || n_splits < 2 ||
+      n_splits > kMergeFoldMaxSplits || group_size <= 0 || (H * D) % group_size ||
+      group_size % 32 || (act_dtype != SF_F16 && act_dtype != SF_BF16 && act_dtype != SF_F32))
+    return 0;
+  BlkPlan p;
+  return plan_blk(B, N, H * D, group_size, act_dtype, PRE_MERGE, false, &p) ? 1 : 0;
+}
+
+extern "C" int sf_q4_gemv_attn_merge(const void *blob, const void *workspace,
+                                     size_t workspace_bytes, int n_splits, int H, int D,
+                                     int act_dtype, void *y, int y_dtype, float *y_f32,
+                                     const void *bias, int bias_dtype, int B, int N,
+                                     int group_size, int has_zeros, void *stream) {
+  const int K = H * D;
+  int rc = check_shape(N, K, group_size);
+  if (rc) return rc;
+  SF_REQUIRE(blob && workspace && (y || y_f32), SF_EINVAL, "null pointer argument");
+  if ((rc = check_out(y_dtype, bias, bias_dtype))) return rc;
+  SF_REQUIRE(((uintptr_t)blob & 255) == 0 && ((uintptr_t)workspace & 255) == 0, SF_EINVAL,
+             "blob and workspace must be 256-byte aligned");
+  SF_REQUIRE(sf_q4_gemv_attn_merge_supported(B, N, H, D, n_splits, group_size, act_dtype),
+             SF_EUNSUPPORTED,
+             "folded attention merge at batch %d (N=%d H=%d head_dim=%d splits=%d group_size=%d "
+             "act dtype %d): not taken by this GEMV; run sf_attn_decode_i8kv and sf_q4_gemv "
+             "instead",
+             B, N, H, D, n_splits, group_size, act_dtype);
+  size_t acc_off, ml_off;
+  const size_t need = sf_split_ws_parts(B * H, D, n_splits, &acc_off, &ml_off);
+  SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "attention workspace too small: %zu < %zu",
+             workspace_bytes, need);
+  GemvArgs args = make_args(blob, (const char *)workspace + acc_off, y, y_dtype, y_f32, bias,
+                            bias_dtype, B, N, K, group_size, has_zeros, stream);
+  args.mml = (const float *)((const char *)workspace + ml_off);
+  args.ms = n_splits;
+  args.md = D;
+  BlkPlan p;
+  plan_blk(B, N, K, group_size, act_dtype, PRE_MERGE, false, &p);
+  launch(p, args, act_dtype, PRE_MERGE, nullptr, 0.f);
+  return sf_check_launch("sf_q4_gemv_attn_merge");
+}
+
 extern "C" int sf_q4_gemv_fused_rope_supported(int N, int K, int group_size, int H, int KVH, int D,
                                                int act_dtype) {
   if (N <= 0 || K <= 0 || group_size <= 0 || K % group_size || group_size % 32 || H <= 0 ||

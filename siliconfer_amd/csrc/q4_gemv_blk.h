@@ -45,9 +45,12 @@
 //  * XL: the workgroup stages x in LDS once (fp16 / bf16 as they are; fp32 as
 //    high and low bf16 rows; zero past K), loading it before the weight stream
 //    and storing it after; A fragments are LDS reads. A folded producer
-//    (PRE_RMSNORM / PRE_SILU) computes the activations while staging them,
-//    rounded as sf_rmsnorm / sf_silu_mul would store them, so a fused launch
-//    gives the same bits as the producer followed by the plain GEMV.
+//    (PRE_RMSNORM / PRE_SILU / PRE_MERGE) computes the activations while
+//    staging them, rounded as sf_rmsnorm / sf_silu_mul / the attention's merge
+//    launch would store them, so a fused launch gives the same bits as the
+//    producer followed by the plain GEMV. PRE_MERGE combines split-T attention
+//    partials (split_merge.h) into the o-projection's input, one 8-dim piece
+//    per thread with every split's loads in flight before the weights.
 //  * direct: every lane loads its own fragments (buffer loads; rows >= B and k
 //    >= K read past the resource and return zero without touching memory),
 //    the first XR units ahead of the weights and the rest in a ring. Used for
@@ -57,13 +60,14 @@
 #include <stdlib.h>
 
 #include "sf_common.h"
+#include "split_merge.h"
 
 namespace sf_gemv {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SILU = 2;
+constexpr int PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SILU = 2, PRE_MERGE = 3;
 constexpr int kMaxWaves = 16;
 constexpr int kUnitK = 128;             // k per weight unit (16 rows x 64 bytes)
 constexpr int kXlMaxBytes = 80 * 1024;  // LDS budget of the staged activations (two workgroups per CU)
@@ -128,16 +132,23 @@ struct BlkArgs {
   int xp;             // LDS row pitch of the staged activations (elements)
   const float *pre_w; // RMSNorm weight (PRE_RMSNORM)
   float eps;
+  const float *mml;   // PRE_MERGE: split (m, l) pairs (x is the split acc)
+  int ms, md;         // PRE_MERGE: splits, head_dim
 };
 
 // Activations staged per thread in XL mode, in pieces of 8 consecutive k of one
 // batch row: 16 bytes of fp16 / bf16, 32 of fp32, and 64 (source + weight / up
-// half) for a folded producer.
+// half) for the folded RMSNorm / SwiGLU; the folded merge holds its split
+// partials apart, one piece per thread.
 template <int XDT, int PRE>
 struct XPiece {
-  static constexpr int NQ = PRE != PRE_NONE ? 4 : XDT == SF_F32 ? 2 : 1;  // 16-byte loads
-  static constexpr int PER_THREAD = PRE != PRE_NONE ? 2 : XDT == SF_F32 ? 2 : 4;
+  static constexpr int NQ = PRE == PRE_MERGE ? 1 : PRE != PRE_NONE ? 4 : XDT == SF_F32 ? 2 : 1;  // 16-byte loads
+  static constexpr int PER_THREAD = PRE == PRE_MERGE ? 1 : PRE != PRE_NONE ? 2 : XDT == SF_F32 ? 2 : 4;
 };
+
+inline int pieces_per_thread(int pre, int xdt) {
+  return pre == PRE_MERGE ? 1 : pre != PRE_NONE ? 2 : xdt == SF_F32 ? 2 : 4;
+}
 
 // fp32 -> (bf16 high, bf16 remainder) of two values, packed in pairs (the GEMM's split).
 __device__ __forceinline__ void split_pair(float a, float b, uint32_t &hi, uint32_t &lo) {
@@ -277,7 +288,28 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   };
   u32x4 xq[XL ? XP::PER_THREAD : 1][XP::NQ];
   SfRowNorm nrm;
-  if constexpr (XL) {
+  // folded merge: (m, l) and 8 acc values of each split for the thread's piece
+  // (threads without a piece and splits past the last load nothing)
+  constexpr int MS = PRE == PRE_MERGE ? kMergeFoldMaxSplits : 1;
+  float2_t mq[MS];
+  u32x4 aq[MS][2];
+  if constexpr (PRE == PRE_MERGE) {
+    if (tid < B * kpr) {
+      const int b = piece_row(tid), k = 8 * (tid - b * kpr);
+      const int h = k / a.md;
+      const size_t row = (size_t)b * (K / a.md) + h;
+      const int d0 = k - h * a.md;
+#pragma unroll
+      for (int s = 0; s < MS; ++s)
+        if (s < a.ms) {
+          const size_t ps = row * a.ms + s;
+          mq[s] = *(const float2_t *)(a.mml + ps * 2);
+          const u32x4 *src = (const u32x4 *)((const float *)a.x + ps * a.md + d0);
+          aq[s][0] = src[0];
+          aq[s][1] = src[1];
+        }
+    }
+  } else if constexpr (XL) {
 #pragma unroll
     for (int q = 0; q < XP::PER_THREAD; ++q) {
       if (q > 0 && tid + q * NT >= B * kpr) break;  // uniform for all but one wave
@@ -387,7 +419,28 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
       if (p < B * kpr) {
         const int b = piece_row(p), k = 8 * (p - b * kpr);
         float f[8];
-        piece_values<XDT, PRE>(xq[q], PRE == PRE_RMSNORM ? inv_s[b] : 1.f, f);
+        if constexpr (PRE == PRE_MERGE) {
+          float M = -INFINITY;
+#pragma unroll
+          for (int s = 0; s < MS; ++s)
+            if (s < a.ms) M = fmaxf(M, mq[s].x);
+          const float mref = sf_merge_mref(M);
+          float L = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = 0.f;
+#pragma unroll
+          for (int s = 0; s < MS; ++s)
+            if (s < a.ms) {
+              const float w = sf_merge_weight(mq[s].x, mref);
+              L = fmaf(mq[s].y, w, L);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) f[e] = fmaf(sf_bitcast<float>(aq[s][e / 4][e % 4]), w, f[e]);
+            }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = sf_merge_finish(L, f[e]);
+        } else {
+          piece_values<XDT, PRE>(xq[q], PRE == PRE_RMSNORM ? inv_s[b] : 1.f, f);
+        }
         u32x4 hv, lv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -532,6 +585,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 // Units per wave come from a compiled set so that every register array has a
 // compile-time size and every load can be issued before the first MFMA.
 constexpr int kBpwSet[6] = {1, 2, 4, 8, 11, 12};  // 11: K = 11008 (86 units) over 8 waves
+constexpr int kMergeMaxBpw = 4;  // the folded merge: K = H * head_dim up to 64 units
 
 struct BlkPlan {
   int T, BPW, nw, grid, nblk, ntiles, xl, xp, uq, ur, kc;
@@ -563,7 +617,7 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   p->nblk = (K + kUnitK - 1) / kUnitK;
   p->ntiles = (N + 15) / 16;
   const int gk = group_kind(g);
-  const bool wide = B > 4 && p->ntiles >= 512 && p->nblk <= 32 && gk != 2;
+  const bool wide = B > 4 && p->ntiles >= 512 && p->nblk <= 32 && gk != 2 && pre != PRE_MERGE;
   p->T = rope ? 4 : wide ? 4 : 1;
   const int maxb = max_bpw(gk, xdt != SF_F16);
   const size_t xb = xl_bytes(B, xdt, p->nblk);
@@ -608,8 +662,9 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
   // not change any row's summation order)
   if (pre == PRE_RMSNORM && p->T == 1 && p->BPW <= 2 && p->ntiles > 256 * (16 / p->nw)) p->T = 2;
   if (p->nw > max_waves(pre, p->T * p->BPW)) return false;
+  if (pre == PRE_MERGE && p->BPW > kMergeMaxBpw) return false;  // variants compiled up to 4 units
   p->grid = (p->ntiles + p->T - 1) / p->T;
-  const int per_thread = pre != PRE_NONE ? 2 : xdt == SF_F32 ? 2 : 4;
+  const int per_thread = pieces_per_thread(pre, xdt);
   const bool xl_fit = xb <= (size_t)kXlMaxBytes &&
                       (size_t)B * (K / 8) <= (size_t)per_thread * p->nw * 64;
   const bool need_xl = pre != PRE_NONE || xdt == SF_F32;
@@ -624,6 +679,7 @@ inline bool plan_blk(int B, int N, int K, int g, int xdt, int pre, bool rope, Bl
 struct GemvArgs {
   const uint8_t *w; const f16 *st; const uint8_t *zt; const void *x; void *y; int ydt; float *y32;
   const void *bias; int bdt; int B, N, K, G, g; bool asym; hipStream_t s;
+  const float *mml = nullptr; int ms = 0, md = 0;  // the folded merge's (m, l), splits, head_dim
 };
 
 template <int X, bool A, int GK, int T, int BPW, bool XL, int PRE, bool ROPE, bool KC = false>
@@ -639,7 +695,7 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
   }
   const uint32_t gmul = (uint32_t)(((1ull << 30) + g.g - 1) / g.g);
   const BlkArgs ba{g.w, g.st, g.zt, g.x, g.y, g.ydt, g.y32, g.bias, g.bdt, g.B, g.N, g.K, g.G, g.g,
-                   p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps};
+                   p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps, g.mml, g.ms, g.md};
   const SfRopeAppend ra = rope ? *rope : SfRopeAppend{};
   k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE, KC><<<p.grid, p.nw * 64, p.lds, g.s>>>(ba, ra, pos_dev);
 }
@@ -651,9 +707,10 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
 template <int X, bool A, int GK, int T, bool XL, int PRE, bool ROPE>
 void by_bpw(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float eps,
             const SfRopeAppend *rope, const int *pos_dev) {
-  constexpr int MB = T == 4   ? (GK == 2 ? (ROPE ? 2 : 0) : ROPE ? 4 : 2)
-                     : T == 2 ? (GK == 2 ? 2 : 4)
-                              : max_bpw(GK, X != SF_F16);
+  constexpr int MB = T == 4            ? (GK == 2 ? (ROPE ? 2 : 0) : ROPE ? 4 : 2)
+                     : T == 2          ? (GK == 2 ? 2 : 4)
+                     : PRE == PRE_MERGE ? (max_bpw(GK, X != SF_F16) < kMergeMaxBpw ? max_bpw(GK, X != SF_F16) : kMergeMaxBpw)
+                                       : max_bpw(GK, X != SF_F16);
 #define SF_BPW(N)                                                                 \
   case N:                                                                         \
     if constexpr (N <= MB) launch_cfg<X, A, GK, T, N, XL, PRE, ROPE>(p, g, pre_w, eps, rope, pos_dev); \
@@ -694,6 +751,7 @@ void by_mode(const BlkPlan &p, const GemvArgs &g, int pre, const float *pre_w, f
   if (pre == PRE_RMSNORM && p.T == 2) by_bpw<X, A, GK, 2, true, PRE_RMSNORM, false>(p, g, pre_w, eps, rope, pos_dev);
   else if (pre == PRE_RMSNORM) SF_T(true, PRE_RMSNORM);
   else if (pre == PRE_SILU) SF_T(true, PRE_SILU);
+  else if (pre == PRE_MERGE) by_bpw<X, A, GK, 1, true, PRE_MERGE, false>(p, g, nullptr, 0.f, nullptr, nullptr);
   else if (p.xl) SF_T(true, PRE_NONE);
   else if constexpr (X != SF_F32) SF_T(false, PRE_NONE);
 #undef SF_T

@@ -42,12 +42,12 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
-    """Zero-filled attention workspace, one per (device, stream), grown on demand.
-    The kernel leaves its counters at zero after every call, so it is reused."""
+    """Attention workspace (the split partials), one per (device, stream), grown
+    on demand; nothing in it needs clearing between calls."""
     key = (device, stream_handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 

@@ -141,8 +141,18 @@ class LlamaModel:
         self.pos_dev = torch.zeros((1,), dtype=torch.int32, device=dev)
         self.hist = torch.zeros((max_seq + 1,), dtype=torch.int32, device=dev)
         self.attn_splits = int(self.lib.sf_attn_default_splits_d(1, self.KVH, max_seq, self.D))
-        ws = max(self.lib.sf_attn_workspace_bytes(1, self.Hq, self.D, self.attn_splits), 1 << 16)
-        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)   # counters start at zero
+        # decode attention: about 128 cached tokens per split (2..8 splits), the
+        # split merge folded into the o projection's activation load
+        # (sf_q4_gemv_attn_merge); fuse=False runs the same splits through the
+        # merge launch and a plain GEMV, which gives the same bits
+        L0 = layers[0]
+        fold_s = min(8, max(2, -(-max_seq // 128)))
+        self._attn_fold = bool(self.lib.sf_q4_gemv_attn_merge_supported(
+            1, L0.o.out_features, self.Hq, self.D, fold_s, L0.o.group_size, _DT[act_dtype]))
+        self.decode_splits = fold_s if self._attn_fold else self.attn_splits
+        ws = max(self.lib.sf_attn_workspace_bytes(1, self.Hq, self.D, self.attn_splits),
+                 self.lib.sf_attn_workspace_bytes(1, self.Hq, self.D, self.decode_splits), 1 << 16)
+        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         hw = self.lib.sf_lm_head_workspace_bytes(self.V)
         self.head_ws = torch.zeros(hw, dtype=torch.uint8, device=dev)
         # verify rows (speculative decoding): greedy token and logits per row
@@ -152,7 +162,6 @@ class LlamaModel:
         self.rows_ws = torch.zeros(rw, dtype=torch.uint8, device=dev)
         # decode: RoPE + KV append folded into the qkv projection's epilogue
         # where its batch-1 plan gives one head per workgroup (hidden <= 1024)
-        L0 = layers[0]
         self._qkv_rope = bool(fuse and self.lib.sf_q4_gemv_fused_rope_supported(
             L0.qkv.out_features, L0.qkv.in_features, L0.qkv.group_size, self.Hq, self.KVH, self.D,
             _DT[act_dtype]))
@@ -566,13 +575,25 @@ class LlamaModel:
                     self._rmsnorm(self.h, None, L.w_in, self.xn, 1)
                     self._gemv(L.qkv, self.xn, self.qkv, L.qkv_bias)
                 self._rope_append(l, self.qkv, self.q, 1, pos, 0)
-            self._chk(lib.sf_attn_decode_i8kv_dev(
-                self.q.data_ptr(), _DT[self.q.dtype], self.k_codes[l].data_ptr(),
-                self.k_scales[l].data_ptr(), self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(),
-                _lib.SF_F16, self.attn.data_ptr(), _DT[self.attn.dtype], self.attn_ws.data_ptr(),
-                self.attn_ws.numel(), 1, self.Hq, self.KVH, pos, 1, self.max_seq, self.max_seq,
-                self.D, self.scale, self.attn_splits, st), "sf_attn_decode_i8kv_dev")
-            self._gemv(L.o, self.attn, self.h, self.h)        # residual add as the bias
+            kv = (self.q.data_ptr(), _DT[self.q.dtype], self.k_codes[l].data_ptr(),
+                  self.k_scales[l].data_ptr(), self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(),
+                  _lib.SF_F16)
+            if fuse and self._attn_fold:  # split partials; the merge rides in the o projection
+                self._chk(lib.sf_attn_decode_i8kv_partials_dev(
+                    *kv, self.attn_ws.data_ptr(), self.attn_ws.numel(), 1, self.Hq, self.KVH, pos, 1,
+                    self.max_seq, self.max_seq, self.D, self.scale, self.decode_splits, st),
+                    "sf_attn_decode_i8kv_partials_dev")
+                self._chk(lib.sf_q4_gemv_attn_merge(
+                    L.o.blob.data_ptr(), self.attn_ws.data_ptr(), self.attn_ws.numel(),
+                    self.decode_splits, self.Hq, self.D, _DT[self.act_dtype], None, _lib.SF_F32,
+                    self.h.data_ptr(), self.h.data_ptr(), _lib.SF_F32, 1, L.o.out_features,
+                    L.o.group_size, int(L.o.has_zeros), st), "sf_q4_gemv_attn_merge")
+            else:
+                self._chk(lib.sf_attn_decode_i8kv_dev(
+                    *kv, self.attn.data_ptr(), _DT[self.attn.dtype], self.attn_ws.data_ptr(),
+                    self.attn_ws.numel(), 1, self.Hq, self.KVH, pos, 1, self.max_seq, self.max_seq,
+                    self.D, self.scale, self.decode_splits, st), "sf_attn_decode_i8kv_dev")
+                self._gemv(L.o, self.attn, self.h, self.h)    # residual add as the bias
             if fuse:  # RMSNorm, then SwiGLU, folded into the next projections
                 self._gemv_fused(L.gate_up, self.h, _lib.SF_PRE_RMSNORM, L.w_post, self.gu, None)
                 self._gemv_fused(L.down, self.gu, _lib.SF_PRE_SILU_MUL, None, self.h, self.h)

@@ -109,8 +109,12 @@ def test_gemm_workspace_and_validation():
 
 def test_attention_validation_and_sizes():
     lib = _lib.load()
-    acc = 14 * 256 * 64 * 4
-    assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == 16384 + acc + 14 * 256 * 2 * 4
+    acc = 14 * 256 * 64 * 4  # split acc, then (m, l) at the next 256-byte boundary
+    assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == acc + 14 * 256 * 2 * 4
+    assert lib.sf_attn_workspace_bytes(1, 14, 64, 3) == 10752 + 14 * 3 * 2 * 4
+    rc = lib.sf_attn_decode_i8kv_partials_dev(None, 0, None, None, None, None, 1, None, 0, 1, 14, 2,
+                                              None, 0, 16, 16, 64, 0.1, 1, None)
+    assert rc == -1 and "null pointer" in _lib.last_error()
     rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
                                  1, 14, 2, 16, 16, 512, 0.1, 1, None)
     assert rc == -1 and "exceeds kernel's compile-time max 256" in _lib.last_error()
@@ -120,10 +124,10 @@ def test_attention_validation_and_sizes():
     assert lib.sf_attn_default_splits(1, 2, 16384) == 64
     assert lib.sf_attn_default_splits(1, 2, 4096) == 32
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
-    assert lib.sf_attn_default_splits(1, 2, 1280) == 1 and lib.sf_attn_default_splits(1, 2, 1281) == 11
-    assert lib.sf_attn_default_splits_d(1, 2, 1280, 64) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 640, 128) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 641, 128) == 6
+    assert lib.sf_attn_default_splits(1, 2, 896) == 1 and lib.sf_attn_default_splits(1, 2, 897) == 16
+    assert lib.sf_attn_default_splits_d(1, 2, 896, 64) == 1
+    assert lib.sf_attn_default_splits_d(1, 2, 448, 128) == 1
+    assert lib.sf_attn_default_splits_d(1, 2, 449, 128) == 16
 
 
 def test_kv_append_validation():
@@ -200,6 +204,38 @@ def test_fused_rows_support_and_validation():
     assert lib.sf_q4_gemv_fused_rows(*args(9)) == -1
     assert lib.sf_q4_gemv_fused_rows(*args(5, SILU, 896, 4864)) == -2
     assert "run sf_rmsnorm" in _lib.last_error()
+
+
+def test_attn_merge_fold_support_and_validation():
+    """sf_q4_gemv_attn_merge: 2..8 splits, head_dim a multiple of 8, the GEMV's
+    plans with at most four units per wave; everything else is refused before
+    any launch."""
+    lib = _lib.load()
+    ok = lib.sf_q4_gemv_attn_merge_supported
+    F16, BF16, F32 = _lib.SF_F16, _lib.SF_BF16, _lib.SF_F32
+    for S in range(2, 9):
+        for act in (F16, BF16, F32):
+            assert ok(1, 896, 14, 64, S, 64, act) == 1, (S, act)   # the 0.5B o projection
+    assert ok(1, 896, 14, 64, 1, 64, F16) == 0 and ok(1, 896, 14, 64, 9, 64, F16) == 0
+    assert ok(1, 1024, 8, 128, 5, 128, BF16) == 1
+    assert ok(1, 4096, 32, 128, 8, 128, F16) == 1                 # 7B: K = 4096
+    assert ok(2, 896, 14, 64, 4, 64, F16) == 1
+    assert ok(1, 896, 14, 60, 4, 60, F16) == 0                    # head_dim % 8
+    assert ok(9, 896, 14, 64, 4, 64, F16) == 0
+    assert ok(1, 896, 14, 64, 4, 48, F16) == 0                    # group size off the 32 grid
+    blob = ws = 1 << 20  # never dereferenced: every call below fails its checks first
+    rc = lib.sf_q4_gemv_attn_merge(blob, ws, 1 << 20, 9, 14, 64, F16, None, F32, ws, None, F32, 1,
+                                   896, 64, 0, None)
+    assert rc == -2 and "run sf_attn_decode_i8kv and sf_q4_gemv instead" in _lib.last_error()
+    rc = lib.sf_q4_gemv_attn_merge(blob, ws, 256, 4, 14, 64, F16, None, F32, ws, None, F32, 1,
+                                   896, 64, 0, None)
+    assert rc == -1 and "workspace too small" in _lib.last_error()
+    rc = lib.sf_q4_gemv_attn_merge(blob, ws + 16, 1 << 20, 4, 14, 64, F16, None, F32, ws, None,
+                                   F32, 1, 896, 64, 0, None)
+    assert rc == -1 and "256-byte aligned" in _lib.last_error()
+    rc = lib.sf_attn_decode_i8kv_partials_dev(ws, 1, ws, ws, ws, ws, 1, ws, 1 << 20, 1, 14, 2, ws,
+                                              0, 16, 16, 64, 0.1, 1, None)
+    assert rc == -1 and "partials need 2..512 splits" in _lib.last_error()
 
 
 def test_fused_rope_support():

@@ -148,12 +148,13 @@ def test_max_splits(dev):
 
 
 def test_workspace_reused_across_shapes(dev):
-    """One zero-filled workspace serves calls of different shapes in a row: each
-    call leaves the merge counters (first 16 KiB) back at zero."""
+    """One workspace serves calls of different shapes in a row, and nothing in
+    it needs clearing: it starts filled with 0xFF bytes (NaN floats), which
+    every split's partial overwrites before the merge launch reads it."""
     from siliconfer_amd import _lib
 
     lib = _lib.load()
-    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=dev)
+    ws = torch.full((8 << 20,), 0xFF, dtype=torch.uint8, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     t = lambda a: torch.as_tensor(a).to(dev).contiguous()
     cases = [(2, 20, 2, 64, 1000, 300), (1, 14, 2, 64, 100, 7), (2, 20, 2, 64, 1000, 300),
@@ -170,7 +171,6 @@ def test_workspace_reused_across_shapes(dev):
                                      float(D ** -0.5), S, st)
         _lib.check(rc, "sf_attn_decode_i8kv")
         torch.cuda.synchronize()
-        assert int(ws[:16384].count_nonzero()) == 0, f"counters left set after case {i}"
         ref = A.attention_decode(q, kc, ks, vc, vs)
         assert_close(out.cpu().numpy(), ref, TOL, f"case {i}")
 
@@ -220,19 +220,19 @@ def test_one_split_wave_rounds(dev, T):
 @pytest.mark.parametrize("T", [257, 513, 640])
 def test_one_split_head_dim_128(dev, H, T):
     """One split at head_dim 128 (8 waves, two tiles each in flight): several
-    tile rotations, up to the default one-split limit of 640 tokens."""
+    tile rotations, beyond the default one-split limit of 448 tokens."""
     rng = np.random.default_rng(60 + T + H)
     check(dev, *make_inputs(rng, 1, H, 2, 128, T), n_tiles=1, what=f"D=128 H={H} one split T={T}")
     check(dev, *make_inputs(rng, 1, H, 2, 128, T, np.float16), n_tiles=1,
           what=f"D=128 H={H} one split fp16 scales T={T}")
 
 
-@pytest.mark.parametrize("D,T", [(64, 1280), (64, 1281), (128, 640), (128, 641)])
+@pytest.mark.parametrize("D,T", [(64, 896), (64, 897), (128, 448), (128, 449)])
 def test_default_split_switch(dev, D, T):
     """The default split count on either side of the head_dim-dependent
     one-split limit, through attention_decode's own pick (fp32 and fp16
     scales); default_splits reports the count it uses."""
-    assert (default_splits(1, 2, T, D) == 1) == (T <= (1280 if D == 64 else 640))
+    assert (default_splits(1, 2, T, D) == 1) == (T <= (896 if D == 64 else 448))
     for sdt in (np.float32, np.float16):
         rng = np.random.default_rng(70 + T + D)
         q, kc, ks, vc, vs = make_inputs(rng, 1, 14, 2, D, T, sdt)
