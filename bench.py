@@ -352,6 +352,47 @@ def _config4(dev, lib, timer, cur, out, T):
                                  "launches": "one" if nsp == 1 else "two (split partials, merge)"}
 
 
+def sweep_attn_splits(dev, head_dim=64, Ts=(128, 512, 1024, 4096, 16384),
+                      splits=(1, 2, 8, 16, 32, 64)) -> dict:
+    """Config-4-shaped decode attention (14 / 2 heads, fp16 q, scales and
+    output) over T x split count, graph-timed over cold copies of the cache
+    (up to 256 copies): the measurements behind sf_attn_default_splits_d."""
+    import torch
+
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.Stream(dev)
+    timer = Timer(torch, stream)
+    cur = lambda: torch.cuda.current_stream().cuda_stream
+    q = torch.randn((1, 14, head_dim), device=dev).half()
+    o = torch.empty((1, 14, head_dim), dtype=torch.float16, device=dev)
+    table = {}
+    for T in Ts:
+        kc = torch.randint(-127, 128, (1, 2, T, head_dim), dtype=torch.int8, device=dev)
+        vc = torch.randint(-127, 128, (1, 2, T, head_dim), dtype=torch.int8, device=dev)
+        ks = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+        vs = (torch.rand((1, 2, T), device=dev) * 0.02 + 0.005).half()
+        per = kc.numel() * 2 + ks.numel() * 4
+        n = min(256, max(2, -(-(256 << 20) // per)))
+        sets = [(kc, ks, vc, vs)] + [(kc.clone(), ks.clone(), vc.clone(), vs.clone()) for _ in range(n - 1)]
+        row = {}
+        for S in splits:
+            if S > T:
+                continue
+            wsb = lib.sf_attn_workspace_bytes(1, 14, head_dim, S)
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+            fns = [(lambda a=a, S=S, ws=ws, wsb=wsb: lib.sf_attn_decode_i8kv(
+                q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(), 1,
+                o.data_ptr(), 1, ws.data_ptr(), wsb, 1, 14, 2, T, T, head_dim, 0.125, S, cur()))
+                for a in sets]
+            row[S] = round(min(timer.per_call_us(fns), timer.per_call_us(fns)), 3)
+        table[T] = row
+        del sets
+    return {"attn_split_sweep_us": table, "head_dim": head_dim,
+            "default_splits": {T: int(lib.sf_attn_default_splits_d(1, 2, T, head_dim)) for T in Ts}}
+
+
 def _kv_append(dev, lib, timer, cur, out):
     """KV append: one decode token, [1, 2, 1, 64] fp16 K and V into a 4096-slot cache."""
     import torch
@@ -625,9 +666,10 @@ def profile_kernels(dev) -> None:
     """The timed region's own launches for rocprofv3 (trace or counters):
     PROFILE_WARM + PROFILE_STEPS replays of the captured sweep graphs (the
     summary drops the warm ones), a 256 MiB device copy (read 256 MiB + write
-    256 MiB) that calibrates FETCH_SIZE / WRITE_SIZE, then the secondary
-    kernels' cases (config 1, 2, 4 and the KV append), launched once per cold
-    copy."""
+    256 MiB) that calibrates FETCH_SIZE / WRITE_SIZE, the per-launch floor
+    (graph replays of the empty launch and of the plain reads, as bench.py
+    times them), then the secondary kernels' cases (config 1, 2, 4 and the KV
+    append), launched once per cold copy."""
     import torch
 
     sweep = GpuSweep(dev)
@@ -639,9 +681,87 @@ def profile_kernels(dev) -> None:
         for _ in range(3):
             dst.copy_(src)
     torch.cuda.synchronize()
+    empty, reads = floor_us(dev, sweep.stream, sorted({alg_bytes(N, K, 1) for N, K in SHAPES}))
     secondary(dev, sweep.stream, eager=True)
     print(json.dumps({"profile_kernels": f"{PROFILE_WARM} + {PROFILE_STEPS} graph replays of the "
-                                         "12-case sweep", "calibration_copy_bytes": 256 << 20}))
+                                         "12-case sweep", "calibration_copy_bytes": 256 << 20,
+                      "floor_us_events_under_this_run": {"empty": round(empty, 3),
+                                                         **{str(k): round(v, 3) for k, v in reads.items()}}}))
+
+
+CALIB_BYTES = 256 << 20
+MI355X_SIMDS = 256 * 4
+MI355X_CLOCK_HZ = 2.4e9  # peak engine clock
+
+
+def calibration_copy(dev) -> None:
+    """Three device copies of CALIB_BYTES (read + write CALIB_BYTES each): what
+    FETCH_SIZE / WRITE_SIZE read for them scales every other dispatch's count."""
+    import torch
+
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def summarize_kernels(trace_csv: str, *pmc_csvs: str) -> dict:
+    """Per-kernel summary of a `bench.py --profile-case` run under rocprofv3:
+    durations from the --kernel-trace CSV; from --pmc counter CSVs, the median
+    per dispatch of every counter, HBM bytes (FETCH_SIZE + WRITE_SIZE, each
+    scaled by what it reads for the calibration copy) with the GB/s they give
+    over the mean duration, and the MFMA busy fraction: SQ_VALU_MFMA_BUSY_CYCLES
+    over the cycles of 1024 SIMDs at 2.4 GHz for the mean duration (the CSV
+    sums GRBM_GUI_ACTIVE over its instances, so it is reported, not divided by)."""
+    import csv
+    import statistics
+
+    per = {}
+    for r in csv.DictReader(open(trace_csv)):
+        k = _short_kernel(r["Kernel_Name"])
+        if "copyBuffer" in r["Kernel_Name"]:
+            continue
+        per.setdefault(k, {"dur": [], "ctr": {}})["dur"].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    scale = {}
+    for path in pmc_csvs:
+        rows = list(csv.DictReader(open(path)))
+        for r in rows:
+            name, v = r["Counter_Name"], float(r["Counter_Value"])
+            if "copyBuffer" in r["Kernel_Name"]:
+                if name in ("FETCH_SIZE", "WRITE_SIZE"):
+                    scale[name] = max(scale.get(name, 0.0), v)
+                continue
+            k = _short_kernel(r["Kernel_Name"])
+            per.setdefault(k, {"dur": [], "ctr": {}})["ctr"].setdefault(name, []).append(v)
+    out = {}
+    for k, d in per.items():
+        e = {}
+        if d["dur"]:
+            e.update(n=len(d["dur"]), mean_us=round(statistics.fmean(d["dur"]), 3),
+                     median_us=round(statistics.median(d["dur"]), 3), min_us=round(min(d["dur"]), 3))
+        ctr = {n: statistics.median(v) for n, v in d["ctr"].items()}
+        if ctr:
+            e["counters_median_per_dispatch"] = {n: round(v, 1) for n, v in ctr.items()}
+        if "FETCH_SIZE" in ctr and "WRITE_SIZE" in ctr and scale:
+            ff = CALIB_BYTES / 1024 / scale["FETCH_SIZE"]
+            wf = CALIB_BYTES / 1024 / scale["WRITE_SIZE"]
+            e["fetch_bytes"] = int(ctr["FETCH_SIZE"] * ff * 1024)
+            e["write_bytes"] = int(ctr["WRITE_SIZE"] * wf * 1024)
+            e["calibration"] = {"fetch_scale": round(ff, 4), "write_scale": round(wf, 4)}
+            if "mean_us" in e:
+                e["hbm_GBps"] = round((e["fetch_bytes"] + e["write_bytes"]) / e["mean_us"] / 1e3, 1)
+                e["hbm_frac_of_8TBps"] = round(e["hbm_GBps"] / 8000, 4)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in ctr and "mean_us" in e:
+            e["mfma_busy_frac"] = round(ctr["SQ_VALU_MFMA_BUSY_CYCLES"] /
+                                        (MI355X_SIMDS * e["mean_us"] * 1e-6 * MI355X_CLOCK_HZ), 4)
+        if "SQ_WAIT_INST_ANY" in ctr and "SQ_WAVE_CYCLES" in ctr:
+            e["wave_cycles_waiting_frac"] = round(ctr["SQ_WAIT_INST_ANY"] / ctr["SQ_WAVE_CYCLES"], 4)
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in ctr:
+            e["mfma_bf16_flop"] = int(ctr["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512)
+        out[k] = e
+    return out
 
 
 def _short_kernel(name: str) -> str:
@@ -699,6 +819,16 @@ def summarize_profile(trace_csv=None, fetch_csv=None, write_csv=None) -> dict:
         means = [c["mean_us"] for c in out["cases"] if "mean_us" in c]
         if len(means) == len(cs):
             out["sweep_kernel_sum_us"] = round(sum(means), 3)
+        # the floor kernels of the same run: the empty launch, and the plain
+        # reads by grid size (one per byte count)
+        fl = {}
+        for r in rows:
+            if "k_empty" in r["Kernel_Name"] or "k_read" in r["Kernel_Name"]:
+                key = "empty" if "k_empty" in r["Kernel_Name"] else f"read_grid{r['Grid_Size_X']}"
+                fl.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        if fl:
+            out["floor_traced_us"] = {k: {"n": len(v), "median": round(statistics.median(v), 3),
+                                          "mean": round(statistics.fmean(v), 3)} for k, v in fl.items()}
         copies = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
                   if "copyBuffer" in r["Kernel_Name"]]
         if copies:
@@ -784,12 +914,19 @@ def main() -> int:
                     help="only run the sweep's graph replays and the secondary kernels (for rocprofv3)")
     ap.add_argument("--summarize-e2e", metavar="CSV",
                     help="per-kernel time per token from a kernel trace of --profile-e2e")
+    ap.add_argument("--sweep-attn-splits", type=int, metavar="HEAD_DIM",
+                    help="time config-4-shaped attention over T x split count and exit")
+    ap.add_argument("--summarize-kernels", nargs="+", metavar="CSV",
+                    help="TRACE_CSV [PMC_CSV ...]: per-kernel summary of a --profile-case run")
     ap.add_argument("--summarize-profile", nargs="+", metavar="CSV",
                     help="TRACE_CSV [FETCH_CSV WRITE_CSV]: summarize rocprofv3 output and exit")
     args = ap.parse_args()
 
     if args.summarize_e2e:
         print(json.dumps(summarize_e2e(args.summarize_e2e), indent=1))
+        return 0
+    if args.summarize_kernels:
+        print(json.dumps(summarize_kernels(*args.summarize_kernels), indent=1))
         return 0
     if args.summarize_profile:
         paths = args.summarize_profile + [None] * 3
@@ -809,9 +946,15 @@ def main() -> int:
         raise SystemExit("bench.py needs a gfx950 GPU and the built libsiliconfer_hip.so")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.sweep_attn_splits:
+        d = args.sweep_attn_splits
+        Ts = (128, 512, 1024, 4096, 16384) if d <= 64 else (256, 320, 448, 512, 1024, 4096)
+        print(json.dumps(sweep_attn_splits(dev, d, Ts)))
+        return 0
     if args.profile_case:
         st = torch.cuda.Stream(dev)
         print(json.dumps(secondary(dev, st, only={args.profile_case})))
+        calibration_copy(dev)
         return 0
     if args.profile_kernels:
         profile_kernels(dev)

@@ -1008,14 +1008,17 @@ extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
 
 extern "C" int sf_attn_default_splits_d(int B, int KVH, int T, int D) {
   // One split (one workgroup per kv head, no merge launch) up to 896 tokens at
-  // head_dim 64 and 448 at larger head dims; beyond, about 128 tokens per
-  // split, at least 16 and at most 64 splits. Measured on MI355X at 14 / 2
-  // heads, head_dim 64 (us, one split / best split count): T = 512: 6.6 / 7.9;
-  // 1024: 8.7 / 8.2 (16-32 splits); 4096: 22.5 / 8.9 (32); 16384: 79.5 / 11.0 (64).
+  // head_dim 64 and 320 at larger head dims; beyond, about 128 (head_dim 64) or
+  // 32 (larger) tokens per split, at least 16 and at most 64 splits. Measured
+  // on MI355X at 14 / 2 heads (us, one split / best split count):
+  //   head_dim 64:  T = 512: 6.6 / 7.9;  1024: 8.7 / 8.2 (16-32 splits);
+  //                 4096: 22.5 / 8.9 (32);  16384: 79.5 / 11.0 (64);
+  //   head_dim 128: T = 256: 7.8 / 8.6;  448: 9.9 / 8.8 (16);  1024: 14.7 / 8.9 (32);
+  //                 4096: 43.8 / 10.0 (64).
   (void)B;
   (void)KVH;
-  if (T <= (D <= 64 ? 896 : 448)) return 1;
-  int s = (T + 127) / 128;
+  if (T <= (D <= 64 ? 896 : 320)) return 1;
+  int s = D <= 64 ? (T + 127) / 128 : (T + 31) / 32;
   if (s < 16) s = 16;
   if (s > 64) s = 64;
   return s;

@@ -126,8 +126,10 @@ def test_attention_validation_and_sizes():
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
     assert lib.sf_attn_default_splits(1, 2, 896) == 1 and lib.sf_attn_default_splits(1, 2, 897) == 16
     assert lib.sf_attn_default_splits_d(1, 2, 896, 64) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 448, 128) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 449, 128) == 16
+    assert lib.sf_attn_default_splits_d(1, 2, 320, 128) == 1
+    assert lib.sf_attn_default_splits_d(1, 2, 321, 128) == 16
+    assert lib.sf_attn_default_splits_d(1, 2, 1024, 128) == 32
+    assert lib.sf_attn_default_splits_d(1, 2, 4096, 128) == 64
 
 
 def test_kv_append_validation():

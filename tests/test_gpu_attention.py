@@ -220,19 +220,19 @@ def test_one_split_wave_rounds(dev, T):
 @pytest.mark.parametrize("T", [257, 513, 640])
 def test_one_split_head_dim_128(dev, H, T):
     """One split at head_dim 128 (8 waves, two tiles each in flight): several
-    tile rotations, beyond the default one-split limit of 448 tokens."""
+    tile rotations, beyond the default one-split limit of 320 tokens."""
     rng = np.random.default_rng(60 + T + H)
     check(dev, *make_inputs(rng, 1, H, 2, 128, T), n_tiles=1, what=f"D=128 H={H} one split T={T}")
     check(dev, *make_inputs(rng, 1, H, 2, 128, T, np.float16), n_tiles=1,
           what=f"D=128 H={H} one split fp16 scales T={T}")
 
 
-@pytest.mark.parametrize("D,T", [(64, 896), (64, 897), (128, 448), (128, 449)])
+@pytest.mark.parametrize("D,T", [(64, 896), (64, 897), (128, 320), (128, 321)])
 def test_default_split_switch(dev, D, T):
     """The default split count on either side of the head_dim-dependent
     one-split limit, through attention_decode's own pick (fp32 and fp16
     scales); default_splits reports the count it uses."""
-    assert (default_splits(1, 2, T, D) == 1) == (T <= (896 if D == 64 else 448))
+    assert (default_splits(1, 2, T, D) == 1) == (T <= (896 if D == 64 else 320))
     for sdt in (np.float32, np.float16):
         rng = np.random.default_rng(70 + T + D)
         q, kc, ks, vc, vs = make_inputs(rng, 1, 14, 2, D, T, sdt)
