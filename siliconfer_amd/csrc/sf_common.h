@@ -93,11 +93,9 @@ __device__ __forceinline__ float sf_bf16_to_f32(uint16_t b) {
 }
 
 // round-to-nearest-even float -> bf16 bits (NaN kept quiet)
+// fp32 -> bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32; NaN stays NaN)
 __device__ __forceinline__ uint16_t sf_f32_to_bf16(float f) {
-  uint32_t u = sf_bitcast<uint32_t>(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 template <int DT>
