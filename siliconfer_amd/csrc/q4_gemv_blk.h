@@ -90,14 +90,29 @@ struct DequantConsts {
 
 // bias: [N] added to every batch row, or y32 itself (fp32): each output then
 // adds its own previous value (a residual add, per batch row)
+// The addend of output idx (row `row`): bias[row], or with bias == y32 the
+// output's previous value (the residual add).
+__device__ __forceinline__ float bias_value(const void *bias, int bdt, const float *y32, size_t idx,
+                                            int row) {
+  if (bias == y32) return y32[idx];
+  if (bdt == SF_F32) return ((const float *)bias)[row];
+  if (bdt == SF_F16) return (float)((const f16 *)bias)[row];
+  return sf_bf16_to_f32(((const uint16_t *)bias)[row]);
+}
+
+// Stores v (its addend already added) to y32 and / or y.
+__device__ __forceinline__ void store_sum(void *y, int ydt, float *y32, size_t idx, float v) {
+  if (y32) y32[idx] = v;
+  if (y) {
+    if (ydt == SF_F16) ((f16 *)y)[idx] = (f16)v;
+    else if (ydt == SF_BF16) ((uint16_t *)y)[idx] = sf_f32_to_bf16(v);
+    else ((float *)y)[idx] = v;
+  }
+}
+
 __device__ __forceinline__ void store_out(void *y, int ydt, float *y32, const void *bias, int bdt,
                                           size_t idx, int row, float v) {
-  if (bias) {
-    if (bias == y32) v += y32[idx];
-    else if (bdt == SF_F32) v += ((const float *)bias)[row];
-    else if (bdt == SF_F16) v += (float)((const f16 *)bias)[row];
-    else v += sf_bf16_to_f32(((const uint16_t *)bias)[row]);
-  }
+  if (bias) v += bias_value(bias, bdt, y32, idx, row);
   if (y32) y32[idx] = v;
   if (y) {
     if (ydt == SF_F16) ((f16 *)y)[idx] = (f16)v;
@@ -332,6 +347,20 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     if constexpr (PRE == PRE_RMSNORM)
       if (wave < B) nrm.issue<true>((const float *)a.x + (size_t)wave * K, nullptr, K);
   }
+  // ---- the epilogue's operands, loaded now so that the epilogue waits on no
+  // round trip of its own: the addend of each output (when every output has a
+  // thread of its own: thread e stores output e) and the RoPE position
+  const int n_out = B * T * 16;
+  const bool out_pre = n_out <= NT;
+  float addend = 0.f;
+  if (out_pre && tid < n_out && a.bias) {
+    const int b = tid / (T * 16), row = n0 + tid - b * (T * 16);
+    if (row < a.N) addend = bias_value(a.bias, a.bdt, a.y32, (size_t)b * a.N + row, row);
+  }
+  int rpos = 0;
+  if constexpr (ROPE) rpos = *pos_dev;
+  const bool rope_ok = ROPE && rpos >= 0 && rpos < rope.T_cap && rpos < rope.max_pos;
+  SfRopeCS rcs{};
   __amdgpu_buffer_rsrc_t xrs;
   int xoff = 0;
   u32x4 xs[XR][4];
@@ -401,6 +430,10 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   // every load above goes out before any math (the scheduler would otherwise
   // hold some back behind the first waits to save registers)
   __builtin_amdgcn_sched_barrier(0);
+  // the RoPE table rows at the position (after the weights: they need the
+  // position's value, and arrive long before the epilogue)
+  if constexpr (ROPE)
+    if (c == 0 && tid < 64 && rope_ok) rcs = sf_rope_load_cs(rope, rpos);
 
   // ---- XL (first chunk): finish the producer, stage the activations, sync
   if constexpr (XL) if (c == 0) {
@@ -551,31 +584,28 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   __syncthreads();
   if constexpr (ROPE) {
     float *hv = red + nw * 8 * (T * 16);  // the head's 64 outputs, bias added
-    if (tid < 64) {
+    if (tid < 64) {  // B = 1, 64 outputs: out_pre holds
       float v = 0.f;
       for (int wi = 0; wi < nw; ++wi) v += red[(wi * 8) * (T * 16) + tid];
-      if (a.bias) {
-        const int row = n0 + tid;
-        if (a.bdt == SF_F32) v += ((const float *)a.bias)[row];
-        else if (a.bdt == SF_F16) v += (float)((const f16 *)a.bias)[row];
-        else v += sf_bf16_to_f32(((const uint16_t *)a.bias)[row]);
-      }
+      if (a.bias) v += addend;
       hv[tid] = v;
     }
     __syncthreads();
-    if (tid < 64) {
-      const int pos = *pos_dev;
-      if (pos >= 0 && pos < rope.T_cap && pos < rope.max_pos) sf_rope_append_head(rope, hv, blockIdx.x, pos, 0);
-    }
+    if (tid < 64 && rope_ok) sf_rope_append_head(rope, hv, blockIdx.x, rpos, 0, rcs);
     return;
   }
-  for (int e = tid; e < B * T * 16; e += NT) {
+  for (int e = tid; e < n_out; e += NT) {
     const int b = e / (T * 16), c = e - b * (T * 16);
     const int row = n0 + c;
     if (row >= a.N) continue;
     float v = 0.f;
     for (int wi = 0; wi < nw; ++wi) v += red[(wi * 8 + b) * (T * 16) + c];
-    store_out(a.y, a.ydt, a.y32, a.bias, a.bdt, (size_t)b * a.N + row, row, v);
+    if (out_pre) {
+      if (a.bias) v += addend;
+      store_sum(a.y, a.ydt, a.y32, (size_t)b * a.N + row, v);
+    } else {
+      store_out(a.y, a.ydt, a.y32, a.bias, a.bdt, (size_t)b * a.N + row, row, v);
+    }
   }
 }
 

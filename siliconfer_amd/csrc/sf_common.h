@@ -293,12 +293,37 @@ __device__ __forceinline__ void sf_store_dt(void *p, int dt, size_t i, float v) 
   else ((uint16_t *)p)[i] = sf_f32_to_bf16(v);
 }
 
+// The cos / sin table entries of the lane's dims at `pos` (lane + 64 j < D / 2),
+// for a caller that issues them ahead of the rotation.
+struct SfRopeCS {
+  static constexpr int MAXP = 2;  // D <= 256
+  float c[MAXP], s[MAXP];
+};
+
+__device__ __forceinline__ SfRopeCS sf_rope_load_cs(const SfRopeAppend &a, int pos) {
+  const int lane = threadIdx.x & 63, half = a.D >> 1;
+  SfRopeCS r;
+#pragma unroll
+  for (int j = 0; j < SfRopeCS::MAXP; ++j) {
+    const int d = lane + 64 * j;
+    r.c[j] = r.s[j] = 0.f;
+    if (d < half) {
+      r.c[j] = a.cos_t[(size_t)pos * half + d];
+      r.s[j] = a.sin_t[(size_t)pos * half + d];
+    }
+  }
+  return r;
+}
+
+// One head's rotate-half RoPE at `pos` (q and k heads; v passes through) from
+// its D fp32 values x, then q to q_out row `row`, or k / v quantized into the
+// cache row `pos` (abs-max / 127 per vector, round half to even, clip).
 __device__ __forceinline__ void sf_rope_append_head(const SfRopeAppend &a, const float *x, int head,
-                                                    int pos, int row) {
+                                                    int pos, int row, const SfRopeCS &cs) {
   const int lane = threadIdx.x & 63;
   const int D = a.D, half = D >> 1;
   const bool is_q = head < a.H, is_k = !is_q && head < a.H + a.KVH;
-  constexpr int MAXP = 2;  // D <= 256
+  constexpr int MAXP = SfRopeCS::MAXP;
   float lo[MAXP], hi[MAXP];
 #pragma unroll
   for (int j = 0; j < MAXP; ++j) {
@@ -309,7 +334,7 @@ __device__ __forceinline__ void sf_rope_append_head(const SfRopeAppend &a, const
       if (is_q || is_k) {
         // separately rounded products, as x * cos + rotate(x) * sin in fp32
 #pragma clang fp contract(off)
-        const float c = a.cos_t[(size_t)pos * half + d], s = a.sin_t[(size_t)pos * half + d];
+        const float c = cs.c[j], s = cs.s[j];
         lo[j] = u * c - w * s;
         hi[j] = w * c + u * s;
       } else {
@@ -347,6 +372,11 @@ __device__ __forceinline__ void sf_rope_append_head(const SfRopeAppend &a, const
     }
   }
   if (lane == 0) sf_store_dt(is_k ? a.k_scales : a.v_scales, a.scale_dtype, crow, s);
+}
+
+__device__ __forceinline__ void sf_rope_append_head(const SfRopeAppend &a, const float *x, int head,
+                                                    int pos, int row) {
+  sf_rope_append_head(a, x, head, pos, row, sf_rope_load_cs(a, pos));
 }
 
 // silu(g) * u as the decoder computes it (one formula for every kernel):
