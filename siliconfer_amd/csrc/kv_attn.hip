@@ -433,8 +433,13 @@ constexpr int attn_mfma_smem_floats() {
 // (b, kv head) runs 16 waves with one tile each in flight at head_dim 64 (more
 // tiles per wave spill at 128 VGPRs) and 8 waves with 2 at head_dim 128, so a
 // 512-token cache is one round of loads and needs no cross-workgroup merge.
-// Splits start on 32-token boundaries (tile rounded up to a multiple of 32), so
-// when T_cap % 4 == 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
+// The cache's 32-token tiles go round robin: split s takes tiles s, s + S,
+// s + 2 S, ..., and its wave w every NW-th of those (tile j = s + S (w + NW i)).
+// Which tiles a wave owns does not depend on the cache length, so a wave's
+// first NB tiles are loaded before the length (device memory on the decode
+// path) has arrived; rows are clamped into the cache and tokens at or past the
+// length are masked. Tiles start on 32-token boundaries, so when T_cap % 4 ==
+// 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
 template <int QDT, int SDT, int D, int NW, int NB>
 __global__ void __launch_bounds__(NW * 64)
 k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
@@ -458,12 +463,8 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane & 15, g = lane >> 4;
-  int Tv = T_dev ? *T_dev + T : T;
-  if (causal) Tv = (T_dev ? *T_dev : T) + b + 1;
-  Tv = max(0, min(Tv, T_cap));
-  const int tile = ((Tv + n_splits - 1) / n_splits + 31) & ~31;
-  const int t0 = min(split * tile, Tv), t1 = min(t0 + tile, Tv);
   const size_t base = ((size_t)(causal ? 0 : b) * KVH + kvh) * (size_t)T_cap;
+  const int jstep = n_splits * NW, j0 = split + n_splits * wave;  // this wave's tiles j0 + jstep i
   const size_t bh0 = (size_t)b * H + (size_t)kvh * G;
 
   // q as the B operand of S^T = K q^T: lane (head hl, group g), k-step ks:
@@ -486,13 +487,14 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     u32x4 v[VC];         // V chunks for the LDS stage
     float ks[8], vs[8];  // scales of the lane's tokens T_g (as loaded; masked later)
   };
-  const int ntiles = t1 > t0 ? (t1 - t0 + 31) / 32 : 0;
   auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
+  // tile j's rows (clamped into the cache: a tile is loaded before the length
+  // is known, and its tokens past the length are masked in compute)
   auto load = [&](int j, Tile &tl) {
-    const int tb = t0 + 32 * j;
+    const int tb = 32 * j;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
-      const int t = min(tb + 16 * h2 + hl, t1 - 1);
+      const int t = min(tb + 16 * h2 + hl, T_cap - 1);
       const u32x4 *kp = (const u32x4 *)(kc + (base + t) * D + g * (D / 4));
 #pragma unroll
       for (int c = 0; c < KW / 4; ++c) tl.k[h2][c] = kp[c];
@@ -500,7 +502,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
 #pragma unroll
     for (int c = 0; c < VC; ++c) {
       const int ch = lane + 64 * c, tok = ch / (D / 16), piece = ch % (D / 16);
-      const int t = min(tb + tok, t1 - 1);
+      const int t = min(tb + tok, T_cap - 1);
       tl.v[c] = *(const u32x4 *)(vc + (base + t) * D + piece * 16);
     }
     if (vscale) {
@@ -533,12 +535,23 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const size_t row = base + min(tb + tok_of(r), t1 - 1);
+        const size_t row = base + min(tb + tok_of(r), T_cap - 1);
         tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
         tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
       }
     }
   };
+
+  // the wave's first tiles (those that start inside the cache), then the length
+  Tile tl[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (32 * (j0 + jstep * u) < T_cap) load(j0 + jstep * u, tl[u]);
+  int Tv = T_dev ? *T_dev + T : T;
+  if (causal) Tv = (T_dev ? *T_dev : T) + b + 1;
+  Tv = max(0, min(Tv, T_cap));
+  const int ntot = (Tv + 31) / 32;  // tiles holding tokens
+  const int mine = j0 < ntot ? (ntot - j0 + jstep - 1) / jstep : 0;
 
   uint8_t *vt = (uint8_t *)smem + wave * 32 * PITCH;
   float m = -INFINITY, lsum = 0.f;
@@ -547,7 +560,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   for (int d = 0; d < DB; ++d) O[d] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int j, const Tile &tl) {
-    const int tb = t0 + 32 * j;
+    const int tb = 32 * j;
     // S^T for the two 16-token halves
     float4_t S[2];
 #pragma unroll
@@ -565,7 +578,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const bool valid = tb + tok_of(r) < t1;
+      const bool valid = tb + tok_of(r) < Tv;
       sc[r] = valid ? S[r >> 2][r & 3] * (tl.ks[r] * qscale) : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
@@ -582,7 +595,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
       ps += p;
       // masked tokens weigh exactly 0 (their scale may be any stale value)
-      const float pv = tb + tok_of(r) < t1 ? p * tl.vs[r] : 0.f;
+      const float pv = tb + tok_of(r) < Tv ? p * tl.vs[r] : 0.f;
       ph[r] = (f16)pv;
       pl[r] = (f16)(pv - (float)ph[r]);
     }
@@ -608,20 +621,15 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     }
   };
 
-  // this wave's tiles j = wave + NW i, i < mine; NB of them in flight (slot
+  // this wave's tiles j0 + jstep i, i < mine; NB of them in flight (slot
   // i % NB, compile-time after unrolling)
-  const int mine = wave < ntiles ? (ntiles - wave + NW - 1) / NW : 0;
-  Tile tl[NB];
-#pragma unroll
-  for (int u = 0; u < NB; ++u)
-    if (u < mine) load(wave + NW * u, tl[u]);
   for (int i0 = 0; i0 < mine; i0 += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int i = i0 + u;
       if (i < mine) {
-        compute(wave + NW * i, tl[u]);
-        if (i + NB < mine) load(wave + NW * (i + NB), tl[u]);
+        compute(j0 + jstep * i, tl[u]);
+        if (i + NB < mine) load(j0 + jstep * (i + NB), tl[u]);
       }
     }
   }
