@@ -10,11 +10,12 @@
 //
 // Two kernels, one 128 x 128 output tile per workgroup (the same tiling, so
 // the same split-K choice and workspace):
-//  * k_q4_gemm_w (fp16 / bf16 activations; groups of 32, 64 or a multiple of
-//    128): every operand byte (X fragments, the blob's W units, scales,
+//  * k_q4_gemm_ws (fp16 / bf16 activations; groups of 32, 64 or a multiple
+//    of 128): every operand byte (X fragments, the blob's W units, scales,
 //    zero-points) goes straight into LDS with buffer / global loads ... lds,
-//    four stages deep; waves dequantize their B operands from the raw codes
-//    (described above the kernel).
+//    four stages deep; four convert waves turn the next step's codes into
+//    the exact integers q - z as MFMA B operands in LDS while four math waves
+//    run the MFMAs and the per-group folds (described above the kernel).
 //  * k_q4_gemm (fp32 activations and the other multiples of 32): staging
 //    threads dequantize the W tile once into LDS as the integers q - z (exact
 //    in fp16 and bf16); fp32 activations are split into bf16 high and low
@@ -487,35 +488,39 @@ k_splitk_reduce(const float *__restrict__ part, void *__restrict__ Y, int ydt, f
 }
 
 // ---------------------------------------------------------------------------
-// LDS-streamed GEMM: fp16 / bf16 activations, group sizes 32, 64 and
-// multiples of 128
+// LDS-streamed, wave-specialised GEMM: fp16 / bf16 activations, group sizes
+// 32, 64 and multiples of 128
 // ---------------------------------------------------------------------------
-// The same 128 x 128 output tile on 512 threads; wave w owns rows 32 (w / 2)
-// .. + 31 and columns 64 (w % 2) .. + 63 as two v_mfma_f32_32x32x16 tiles, two
-// waves per SIMD (one's folds and dequantization overlap the other's MFMAs).
-// Every operand byte is fetched once per workgroup, straight into LDS by
-// buffer / global loads ... lds, one of four stages per K step of 64, three
-// steps ahead (step s + 3's loads go out after step s's barrier, into the
-// stage step s - 1 read); a wave's loads per step are 2 X fragments, 1 W unit
-// and, for waves 0..3, one scale or zero-point row:
+// The same 128 x 128 output tile on 512 threads, K steps of 64. Every operand
+// byte is fetched once per workgroup, straight into LDS by buffer / global
+// loads ... lds, one of four stages per step, three steps ahead:
 //  * X: 16 fragments of 1 KB, each one MFMA's A operand in lane order (lane
 //    l: row l % 32, k 8 (l / 32) .. + 7 of a 16-k slice); rows past M and k
 //    past K read as zero.
 //  * W: the tile's 8 units (16 columns x 128 k, 1 KB each, the blob's own
-//    layout) that hold the step's k; a lane's B operand for slice kk of a
-//    32-column block is one dword of its column's unit lane (piece 2 (kk % 2)
-//    + l / 32, 32-k slice 2 (s % 2) + kk / 2).
-//  * the tile's scales (16 cells of 8 fp16) and zero-points (16 cells of 8
+//    layout); the 8 codes of slice kk of a lane's column are one dword of the
+//    column's unit lane (piece 2 (kk % 2) + l / 32, 32-k slice 2 (s % 2) +
+//    kk / 2).
+//  * the scale rows (16 cells of 8 fp16) and zero-point rows (16 cells of 8
 //    nibbles) of the step's groups.
-//  * operands: fp16 activations take the exact q - z (1024 + c minus 1024 + z
-//    in fp16); bf16 ones take 128 + c (exact in bf16) and each group's partial
-//    gives back (128 + z) sum(x) at the fold, sum(x) of every row coming from
-//    one extra MFMA per slice against a ones operand (so it lands in the
-//    accumulators' row layout).
-//  * each group's partial is folded into the result with its fp16 scale once
-//    per group (the reference's grouping, q4_gemv.cpp:136); with groups of 32
-//    and 64 the fold of one group runs beside the next group's MFMAs (two
-//    buffers of partials).
+// The waves split by kind of work, one of each kind per SIMD, so that one
+// wave's MFMAs run beside the other's VALU work (with every wave doing both,
+// the per-step barrier keeps the two waves of a SIMD in the same phase and
+// the two kinds of work take turns):
+//  * waves 0..3 (math): rows 64 (w / 2) .. + 63 and columns 64 (w % 2) ..
+//    + 63 as 2 x 2 v_mfma_f32_32x32x16 tiles; each group's fp32 partial is
+//    folded into the result with its fp16 scale once per group (the
+//    reference's grouping, q4_gemv.cpp:136);
+//  * waves 4..7 (convert): during step s, wave 4 + c turns the codes of
+//    column block c (32 columns) of step s + 1 into the exact integers q - z
+//    as bf16 or fp16 MFMA B operands (lane order) in one of two LDS operand
+//    buffers, which the math waves read in step s + 1.
+// Each wave's loads per step are a fixed count (math wave w: X fragments
+// 4 w .. + 3 and, for w < groups per step, that group's scale row; convert
+// wave 4 + c: W units 2 c, 2 c + 1 and, with zero-points and c < groups per
+// step, that group's zero-point row), so each wait is an exact s_waitcnt
+// vmcnt: a math wave waits for its loads of step s at the top of step s, a
+// convert wave for its loads of step s + 1.
 constexpr int G_BM = 128, G_BN = 128, G_BK = 64, G_THREADS = 512, G_STAGES = 4;
 constexpr int G_FRAG = 1024;                    // one A fragment (32 rows x 16 k)
 constexpr int G_X_BYTES = 16 * G_FRAG;          // a step's X
@@ -525,9 +530,14 @@ template <int NG>
 constexpr int g_z_off() { return G_S_OFF + NG * 1024; }   // zero-points: 256 B per group
 template <int NG>
 constexpr int g_stage_bytes() { return g_z_off<NG>() + NG * 256; }
+// one step's B operands: 4 column blocks x 4 slices x 64 lanes x 16 B
+constexpr int G_B_BYTES = 4 * 4 * 64 * 16;
+template <int NG>
+constexpr int g_lds_bytes() { return G_STAGES * g_stage_bytes<NG>() + 2 * G_B_BYTES; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void gbl_void;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Wait until at most n vector-memory operations of this wave are outstanding
 // (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; exp and lgkm left at their maxima).
@@ -535,8 +545,9 @@ typedef __attribute__((address_space(1))) void gbl_void;
 // The workgroup barrier without __syncthreads' release fence, which would wait
 // for every outstanding load (the loads into LDS count as writes); the asm
 // clobber keeps the compiler from moving memory accesses across it. Ordering
-// is explicit: SF_WAIT_VM before it for this wave's loads, and every LDS read
-// of the previous stage has fed an MFMA or a fold before the wave gets here.
+// is explicit: SF_WAIT_VM before it for this wave's loads, and every LDS
+// access of the previous step has completed (its result feeding an MFMA, a
+// fold or a store) before the wave gets here.
 #define SF_BARRIER()                   \
   do {                                 \
     asm volatile("" ::: "memory");     \
@@ -544,24 +555,39 @@ typedef __attribute__((address_space(1))) void gbl_void;
     asm volatile("" ::: "memory");     \
   } while (0)
 
+// The bf16 B operand of 8 codes (one dword of a unit lane) as the exact
+// integers code - z: the dword's nibble i is k element 2 i (i < 4) or
+// 2 (i - 4) + 1, the pairs the GEMV's dequantization forms
+// ((d >> 4 i) & 0x000F000F); each byte converts to fp32 exactly, and
+// code - z (|.| <= 15) is exact in bf16.
+__device__ __forceinline__ u32x4 dequant_bf16_exact(uint32_t d, float zf) {
+  const uint32_t e = d & 0x0F0F0F0Fu, o = (d >> 4) & 0x0F0F0F0Fu;  // nibbles 0,2,4,6 / 1,3,5,7
+  auto pk = [&](uint32_t v, int b0, int b1) {
+    const float2_t f = {(float)((v >> (8 * b0)) & 0xFFu) - zf, (float)((v >> (8 * b1)) & 0xFFu) - zf};
+    return sf_bitcast<uint32_t>(__builtin_convertvector(f, bf16x2_t));
+  };
+  return u32x4{pk(e, 0, 2), pk(o, 0, 2), pk(e, 1, 3), pk(o, 1, 3)};
+}
+
 template <int XDT, bool ASYM, int GK>
 __global__ void __launch_bounds__(G_THREADS)
-k_q4_gemm_w(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
-            const uint8_t *__restrict__ zt, const void *__restrict__ X, void *__restrict__ Y,
-            int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt,
-            float *__restrict__ part, int M, int N, int K, int G, int g, int ksplit,
-            int steps_per_split, bool vec) {
+k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
+             const uint8_t *__restrict__ zt, const void *__restrict__ X, void *__restrict__ Y,
+             int ydt, float *__restrict__ y32, const void *__restrict__ bias, int bdt,
+             float *__restrict__ part, int M, int N, int K, int G, int g, int ksplit,
+             int steps_per_split, bool vec) {
   static_assert(XDT == SF_F16 || XDT == SF_BF16, "fp16 / bf16 activations");
   constexpr bool BF = XDT == SF_BF16;
   constexpr int NG = GK == 0 ? 2 : 1;  // groups per step (g = 32: two)
   constexpr int SB = g_stage_bytes<NG>(), ZO = g_z_off<NG>();
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // G_STAGES * SB
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // stages, then 2 operand buffers
+  uint8_t *const bops = smem + G_STAGES * SB;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool math = wave < 4;
+  const int cw = wave & 3;                          // index among the waves of its kind
   const int l32 = lane & 31, h = lane >> 5;
-  const int rb = wave >> 1;                        // the wave's row block
-  const int wm = rb * 32, wn = (wave & 1) * 64;    // wave tile origin
   const int m0 = blockIdx.y * G_BM, n0 = blockIdx.x * G_BN;
   const int split = blockIdx.z;
   const int nsteps_total = (K + G_BK - 1) / G_BK;
@@ -571,307 +597,286 @@ k_q4_gemm_w(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   const int ntiles = (N + 15) >> 4, ncells = (N + 7) >> 3;
   const int spg = GK == 2 ? g / G_BK : 1;  // steps per group
 
-  // this wave's loads: X fragments 2w, 2w + 1 (row block w / 2, slices
-  // 2 (w % 2) + 0, 1); W unit w of the tile (clamped to the last row tile);
-  // waves 0..3 one more: 0 / 2 the scales of group 0 / 1, 1 / 3 the
-  // zero-points of group 0 / 1 (when the shape has them)
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)X, 0, M * K * 2, 0x00020000);
-  const int mrow = m0 + rb * 32 + l32;
+  const int mrow = m0 + cw * 32 + l32;  // math wave cw loads row block cw's fragments
   const bool mrow_ok = mrow < M;
-  const int wtile = min((n0 >> 4) + wave, ntiles - 1);
-  const int xq = wave >> 1;  // the group of the extra load (waves 0..3)
-  const bool extra = wave == 0 || (wave == 1 && ASYM) || (wave == 2 && NG == 2) ||
-                     (wave == 3 && ASYM && NG == 2);
-  const bool extra_z = (wave & 1) != 0;
+  const bool extra = math ? cw < NG : (ASYM && cw < NG);
   const int cell = min((n0 >> 3) + (lane & 15), ncells - 1);  // lanes 16.. repeat lane 15's row
   auto issue = [&](int step) {
     const int sc = min(step, s1 - 1);
     uint8_t *stage = smem + (step & 3) * SB;
+    if (math) {
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const int kk = 2 * (wave & 1) + f;
-      const int k = sc * G_BK + kk * 16 + 8 * h;
-      // past the resource (reads zero) unless in range; a select, not a branch
-      const uint32_t in = ((uint32_t)mrow * (uint32_t)K + (uint32_t)k) * 2u;
-      const uint32_t keep = 0u - (uint32_t)(mrow_ok && k < K);
-      const uint32_t off = (in & keep) | (0x80000000u & ~keep);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (2 * wave + f) * G_FRAG), 16,
-                                               off, 0, 0, 0);
+      for (int f = 0; f < 4; ++f) {
+        const int k = sc * G_BK + f * 16 + 8 * h;
+        // past the resource (reads zero) unless in range; a select, not a branch
+        const uint32_t in = ((uint32_t)mrow * (uint32_t)K + (uint32_t)k) * 2u;
+        const uint32_t keep = 0u - (uint32_t)(mrow_ok && k < K);
+        const uint32_t off = (in & keep) | (0x80000000u & ~keep);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (4 * cw + f) * G_FRAG), 16,
+                                                 off, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int wtile = min((n0 >> 4) + 2 * cw + u, ntiles - 1);
+        const uint8_t *unit = wq + ((size_t)wtile * nblk + (sc >> 1)) * 1024 + lane * 16;
+        __builtin_amdgcn_global_load_lds((gbl_void *)unit,
+                                         (lds_void *)(stage + G_W_OFF + (2 * cw + u) * 1024), 16, 0, 0);
+      }
     }
-    const uint8_t *unit = wq + ((size_t)wtile * nblk + (sc >> 1)) * 1024 + lane * 16;
-    __builtin_amdgcn_global_load_lds((gbl_void *)unit, (lds_void *)(stage + G_W_OFF + wave * 1024), 16, 0, 0);
     if (extra) {
-      const int gi = min(GK == 0 ? 2 * sc + xq : GK == 1 ? sc : sc / spg, G - 1);
+      const int gi = min(GK == 0 ? 2 * sc + cw : GK == 1 ? sc : sc / spg, G - 1);
       const size_t c = (size_t)cell * G + gi;
-      if (!extra_z)
-        __builtin_amdgcn_global_load_lds((gbl_void *)(st + c * 8), (lds_void *)(stage + G_S_OFF + xq * 1024), 16, 0, 0);
+      if (math)
+        __builtin_amdgcn_global_load_lds((gbl_void *)(st + c * 8), (lds_void *)(stage + G_S_OFF + cw * 1024),
+                                         16, 0, 0);
       else
-        __builtin_amdgcn_global_load_lds((gbl_void *)(zt + c * 4), (lds_void *)(stage + ZO + xq * 256), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((gbl_void *)(zt + c * 4), (lds_void *)(stage + ZO + cw * 256), 4, 0, 0);
     }
   };
 
-  // a lane's column per column block, and where its unit lane, scale and
-  // zero-point sit in a stage
-  int ncol[2], w_lds[2], s_lds[2], z_lds[2];
+  // ---- convert waves: step t's codes of column block cw into operand buffer t % 2
+  const sf_gemv::DequantConsts dk;
+  auto convert = [&](int t) {
+    const uint8_t *stage = smem + (t & 3) * SB;
+    uint8_t *bo = bops + (t & 1) * G_B_BYTES;
+    const int n = min(n0 + 32 * cw + l32, N - 1);  // past N: column N - 1 (never stored)
+    const int wl = G_W_OFF + ((n >> 4) - (n0 >> 4)) * 1024 + (h * 16 + (n & 15)) * 16 + (t & 1) * 8;
+    const u32x2 lo = *(const u32x2 *)(stage + wl), hi = *(const u32x2 *)(stage + wl + 512);
+    const uint32_t d[4] = {lo.x, hi.x, lo.y, hi.y};  // slices 0..3
+    uint32_t z[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      if constexpr (ASYM)
+        z[q] = (stage[ZO + q * 256 + ((n >> 3) - (n0 >> 3)) * 4 + ((n & 7) >> 1)] >> (4 * (n & 1))) & 15u;
+      else
+        z[q] = 8u;  // offset-binary symmetric codes
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t zq = z[GK == 0 ? kk >> 1 : 0];
+      const u32x4 b = BF ? dequant_bf16_exact(d[kk], (float)zq) : sf_gemv::dequant_f16(d[kk], zq, dk);
+      *(u32x4 *)(bo + (cw * 4 + kk) * 1024 + lane * 16) = b;
+    }
+  };
+
+  // ---- math waves: row blocks 2 (cw / 2) + r, column blocks 2 (cw % 2) + j
+  const int rb0 = 2 * (cw >> 1), cb0 = 2 * (cw & 1);
+  const int wn = 32 * cb0;
+  int s_lds[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int n = min(n0 + wn + 32 * j + l32, N - 1);  // past N: column N - 1 (never stored)
-    ncol[j] = n;
-    w_lds[j] = G_W_OFF + ((n >> 4) - (n0 >> 4)) * 1024 + (h * 16 + (n & 15)) * 16;
+    const int n = min(n0 + wn + 32 * j + l32, N - 1);
     s_lds[j] = G_S_OFF + ((n >> 3) - (n0 >> 3)) * 16 + (n & 7) * 2;
-    z_lds[j] = ZO + ((n >> 3) - (n0 >> 3)) * 4 + ((n & 7) >> 1);
   }
-
   const float16_t zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                             0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
-  const sf_gemv::DequantConsts dk;
-  // Two buffers of group partials (and of the rows' sum(x)): a group's fold
-  // runs while the next group's MFMAs fill the other buffer.
-  float16_t acc[2], gp[2][2], xs[2];
+  float16_t acc[2][2], gp[2][2];
 #pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-    xs[bb] = zero16;
-    acc[bb] = zero16;
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) gp[bb][j] = zero16;
-  }
-
-  // a group's scale and -(128 + z) per column block, read from a stage
-  struct Fold {
-    float s[2], zc[2];
+    for (int j = 0; j < 2; ++j) acc[r][j] = gp[r][j] = zero16;
+  // acc += s * partial, s the group's scale of the lane's column
+  auto fold = [&](const uint8_t *stage, int q) {
+    float sc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sc[j] = (float)*(const f16 *)(stage + s_lds[j] + q * 1024);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[r][j][e] = fmaf(gp[r][j][e], sc[j], acc[r][j][e]);
   };
-  auto zero_point = [&](const uint8_t *stage, int j, int q) -> uint32_t {
-    if constexpr (!ASYM) return 8u;  // offset-binary symmetric codes
-    else return (stage[z_lds[j] + q * 256] >> (4 * (ncol[j] & 1))) & 15u;
-  };
-  auto group_fold = [&](const uint8_t *stage, int q) {
-    Fold f;
+  // one 16-k slice (open: the slice starts its group)
+  auto slice = [&](const uint8_t *stage, const uint8_t *bo, int kk, bool open) {
+    u32x4 a[2], b[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      f.s[j] = (float)*(const f16 *)(stage + s_lds[j] + q * 1024);
-      f.zc[j] = -(float)(128u + zero_point(stage, j, q));
-    }
-    return f;
-  };
-  // acc += s * (partial - (128 + z) sum(x)) (bf16 operands), s * partial (fp16)
-  auto fold = [&](int bb, const Fold &f) {
+    for (int r = 0; r < 2; ++r) a[r] = *(const u32x4 *)(stage + ((rb0 + r) * 4 + kk) * G_FRAG + lane * 16);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j) b[j] = *(const u32x4 *)(bo + ((cb0 + j) * 4 + kk) * 1024 + lane * 16);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float v = BF ? fmaf(f.zc[j], xs[bb][e], gp[bb][j][e]) : gp[bb][j][e];
-        acc[j][e] = fmaf(v, f.s[j], acc[j][e]);
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float16_t cin = open ? zero16 : gp[r][j];
+        if constexpr (BF)
+          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf_bitcast<bf16x8_t>(a[r]),
+                                                             sf_bitcast<bf16x8_t>(b[j]), cin, 0, 0, 0);
+        else
+          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sf_bitcast<half8_t>(a[r]),
+                                                            sf_bitcast<half8_t>(b[j]), cin, 0, 0, 0);
       }
   };
-  // the step's W dwords of each column block: slices (0, 2) and (1, 3)
-  struct WOps {
-    u32x2 lo[2], hi[2];
-  };
-  auto w_ops = [&](const uint8_t *stage, int step) {
-    WOps w;
-    const int jo = (step & 1) * 8;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      w.lo[j] = *(const u32x2 *)(stage + w_lds[j] + jo);
-      w.hi[j] = *(const u32x2 *)(stage + w_lds[j] + 512 + jo);
-    }
-    return w;
-  };
-  // one 16-k slice into buffer bb (open: the slice starts its group)
-  auto slice = [&](const uint8_t *stage, const WOps &w, int kk, int bb, bool open, int q) {
-    uint32_t zq[2] = {0u, 0u};
-    if constexpr (!BF) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) zq[j] = zero_point(stage, j, q);
-    }
-    const u32x4 a = *(const u32x4 *)(stage + (rb * 4 + kk) * G_FRAG + lane * 16);
-    u32x4 b[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t d = kk == 0 ? w.lo[j].x : kk == 1 ? w.hi[j].x : kk == 2 ? w.lo[j].y : w.hi[j].y;
-      b[j] = BF ? sf_gemv::dequant_bf16(d, dk) : sf_gemv::dequant_f16(d, zq[j], dk);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float16_t cin = open ? zero16 : gp[bb][j];
-      if constexpr (BF)
-        gp[bb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            sf_bitcast<bf16x8_t>(a), sf_bitcast<bf16x8_t>(b[j]), cin, 0, 0, 0);
-      else
-        gp[bb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            sf_bitcast<half8_t>(a), sf_bitcast<half8_t>(b[j]), cin, 0, 0, 0);
-    }
-    if constexpr (BF)
-      xs[bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          sf_bitcast<bf16x8_t>(a), sf_bitcast<bf16x8_t>(ones), open ? zero16 : xs[bb], 0, 0, 0);
-  };
-  // g = 32 / 64: the previous group's fold (pending) overlaps this step's
-  // first slices; g >= 128: a group spans g / 64 steps in buffer 0 and is
-  // folded in its last step. `iss` (the loads of a later step) runs after the
-  // second slice, among the MFMAs.
-  Fold pend;
-  bool pending = false;
-  auto compute = [&](int step, int u, auto &&iss) {
+  // `iss` (the loads of a later step) runs after the second slice
+  auto math_step = [&](int step, auto &&iss) {
     const uint8_t *stage = smem + (step & 3) * SB;
-    const WOps w = w_ops(stage, step);
+    const uint8_t *bo = bops + (step & 1) * G_B_BYTES;
     if constexpr (GK == 1) {
-      const int bb = u & 1;
-      slice(stage, w, 0, bb, true, 0);
-      if (pending) fold(bb ^ 1, pend);
-      slice(stage, w, 1, bb, false, 0);
-      pend = group_fold(stage, 0);  // read before the stage can be refilled
+      slice(stage, bo, 0, true);
+      slice(stage, bo, 1, false);
       iss();
-      slice(stage, w, 2, bb, false, 0);
-      slice(stage, w, 3, bb, false, 0);
-      pending = true;
+      slice(stage, bo, 2, false);
+      slice(stage, bo, 3, false);
+      fold(stage, 0);
     } else if constexpr (GK == 0) {
-      slice(stage, w, 0, 0, true, 0);
-      if (pending) fold(1, pend);
-      slice(stage, w, 1, 0, false, 0);
-      const Fold fa = group_fold(stage, 0);
-      pend = group_fold(stage, 1);
+      slice(stage, bo, 0, true);
+      slice(stage, bo, 1, false);
       iss();
-      slice(stage, w, 2, 1, true, 1);
-      fold(0, fa);
-      slice(stage, w, 3, 1, false, 1);
-      pending = true;
+      fold(stage, 0);
+      slice(stage, bo, 2, true);
+      slice(stage, bo, 3, false);
+      fold(stage, 1);
     } else {
       const bool fresh = step % spg == 0 || step == s0;
       const bool last = (step + 1) % spg == 0 || step == s1 - 1;
-      if (fresh) slice(stage, w, 0, 0, true, 0);
-      else slice(stage, w, 0, 0, false, 0);
-      slice(stage, w, 1, 0, false, 0);
-      const Fold f = group_fold(stage, 0);
+      if (fresh) slice(stage, bo, 0, true);
+      else slice(stage, bo, 0, false);
+      slice(stage, bo, 1, false);
       iss();
-      slice(stage, w, 2, 0, false, 0);
-      slice(stage, w, 3, 0, false, 0);
-      if (last) fold(0, f);
+      slice(stage, bo, 2, false);
+      slice(stage, bo, 3, false);
+      if (last) fold(stage, 0);
     }
   };
 
-  // Pipeline. At the top of step s a wave waits until its own loads of step s
-  // have landed: after them went out only its loads of steps s + 1 and s + 2
-  // (3 or 4 per step: a fixed count per wave), so at most that many may be
-  // outstanding. After the barrier every wave's loads of step s are in LDS,
-  // and every wave is done with step s - 1's stage, which step s + 3's loads
-  // (issued during step s) overwrite. Nothing the compiler loads into
-  // registers goes to global memory inside the loop, so these are the only
-  // vector-memory counts.
+  // Pipeline. Loads of step s go out during step s - 3 (the first three in
+  // the prologue) into the stage step s - 4 used; after the barrier at the top
+  // of step s every wave is done with step s - 1's stage and operand buffer
+  // (s + 1) % 2, every math wave's loads of step s and every convert wave's
+  // loads of step s + 1 have landed, and operand buffer s % 2 holds step s's
+  // operands. Nothing the compiler loads into registers goes to global memory
+  // inside the loop, so these loads are the only vector-memory counts.
   if (s0 < s1) {
     issue(s0);
     issue(s0 + 1);
     issue(s0 + 2);
+    if (!math) {  // this wave's loads of step s0 (two later steps' may remain)
+      if (extra) SF_WAIT_VM(6);
+      else SF_WAIT_VM(4);
+    }
+    SF_BARRIER();
+    if (!math) convert(s0);
     for (int s = s0; s < s1; s += 4) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int step = s + u;
         if (step >= s1) break;
-        if (extra) SF_WAIT_VM(8);
-        else SF_WAIT_VM(6);
+        if (math) {
+          if (extra) SF_WAIT_VM(10);
+          else SF_WAIT_VM(8);
+        } else {
+          if (extra) SF_WAIT_VM(3);
+          else SF_WAIT_VM(2);
+        }
         SF_BARRIER();
-        compute(step, u, [&] { issue(step + 3); });
+        if (math) {
+          math_step(step, [&] { issue(step + 3); });
+        } else {
+          issue(step + 3);
+          if (step + 1 < s1) convert(step + 1);
+        }
       }
-    }
-    // the last group's fold (g = 32 / 64): buffer of the last step's parity
-    if constexpr (GK == 1) {
-      if (((s1 - 1 - s0) & 1) == 0) fold(0, pend);
-      else fold(1, pend);
-    } else if constexpr (GK == 0) {
-      fold(1, pend);
     }
   }
 
   // Output: every wave done with the stages and every load landed, then each
-  // wave stages its 32 x 64 tile in its own LDS region and writes it back as
-  // 8-column row segments (16-byte stores). 16-bit outputs without split or
-  // fp32 copy round in registers (bias added first) and stage 16-bit values;
-  // the rest stage fp32 values, one 32-column block at a time.
+  // math wave stages its tile one 32-row block at a time in its own LDS region
+  // and writes it back as 8-column row segments (16-byte stores). 16-bit
+  // outputs without split or fp32 copy round in registers (bias added first)
+  // and stage 16-bit values; the rest stage fp32 values, one 32-column block
+  // at a time.
   SF_WAIT_VM(0);
   __syncthreads();
-  if (ksplit == 1 && !y32 && Y && vec && (ydt == SF_BF16 || ydt == SF_F16)) {
-    constexpr int P16 = 64 + 8;  // halfword pitch of a staged row
-    uint16_t *ot16 = (uint16_t *)smem + wave * 32 * P16;
-    float bc[2] = {0.f, 0.f};
-    if (bias) {
+  if (!math) return;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int cc = min(n0 + wn + 32 * j + l32, N - 1);
-        bc[j] = bdt == SF_F32 ? ((const float *)bias)[cc]
-                : bdt == SF_F16 ? (float)((const f16 *)bias)[cc]
-                                : sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
-      }
-    }
-    const bool obf = ydt == SF_BF16;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float v = acc[j][e] + bc[j];
-        ot16[(8 * (e >> 2) + 4 * h + (e & 3)) * P16 + 32 * j + l32] =
-            obf ? sf_f32_to_bf16(v) : sf_bitcast<uint16_t>((f16)v);
-      }
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int seg = it * 64 + lane;
-      const int rl = seg >> 3, cl = (seg & 7) * 8;
-      const int row = m0 + wm + rl, col = n0 + wn + cl;
-      const u32x4 w8 = *(const u32x4 *)(ot16 + rl * P16 + cl);
-      if (row >= M || col >= N) continue;
-      uint16_t *d = (uint16_t *)Y + (size_t)row * N + col;
-      if (col + 8 <= N) {
-        *(u32x4 *)d = w8;
-      } else {
-        for (int e = 0; e < N - col; ++e) d[e] = (uint16_t)(w8[e >> 1] >> (16 * (e & 1)));
-      }
-    }
-    return;
-  }
-  constexpr int P32 = 32 + 4;  // fp32 pitch of a staged 32-column block
-  float *ot = (float *)smem + wave * 32 * P32;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) ot[(8 * (e >> 2) + 4 * h + (e & 3)) * P32 + l32] = acc[j][e];
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int seg = it * 64 + lane;
-      const int rl = seg >> 2, cl = (seg & 3) * 8;
-      const int row = m0 + wm + rl, col = n0 + wn + 32 * j + cl;
-      float v[8];
-      {
-        const float4_t x0 = *(const float4_t *)(ot + rl * P32 + cl);
-        const float4_t x1 = *(const float4_t *)(ot + rl * P32 + cl + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = x0[e];
-          v[4 + e] = x1[e];
-        }
-      }
-      if (row >= M || col >= N) continue;
-      const int nv = min(8, N - col);
-      const size_t idx = (size_t)row * N + col;
-      if (ksplit > 1) {
-        float *dst = part + (size_t)split * M * N + idx;
-        if (vec && nv == 8) {
-          ((float4_t *)dst)[0] = float4_t{v[0], v[1], v[2], v[3]};
-          ((float4_t *)dst)[1] = float4_t{v[4], v[5], v[6], v[7]};
-        } else {
-          for (int e = 0; e < nv; ++e) dst[e] = v[e];
-        }
-        continue;
-      }
+  for (int r = 0; r < 2; ++r) {
+    const int wm = 32 * (rb0 + r);
+    if (ksplit == 1 && !y32 && Y && vec && (ydt == SF_BF16 || ydt == SF_F16)) {
+      constexpr int P16 = 64 + 8;  // halfword pitch of a staged row
+      uint16_t *ot16 = (uint16_t *)smem + cw * 32 * P16;
+      float bc[2] = {0.f, 0.f};
       if (bias) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int cc = min(col + e, N - 1);
-          if (bdt == SF_F32) v[e] += ((const float *)bias)[cc];
-          else if (bdt == SF_F16) v[e] += (float)((const f16 *)bias)[cc];
-          else v[e] += sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
+        for (int j = 0; j < 2; ++j) {
+          const int cc = min(n0 + wn + 32 * j + l32, N - 1);
+          bc[j] = bdt == SF_F32 ? ((const float *)bias)[cc]
+                  : bdt == SF_F16 ? (float)((const f16 *)bias)[cc]
+                                  : sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
         }
       }
-      store_row8(v, nv, vec, y32, Y, ydt, idx);
+      const bool obf = ydt == SF_BF16;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float v = acc[r][j][e] + bc[j];
+          ot16[(8 * (e >> 2) + 4 * h + (e & 3)) * P16 + 32 * j + l32] =
+              obf ? sf_f32_to_bf16(v) : sf_bitcast<uint16_t>((f16)v);
+        }
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int seg = it * 64 + lane;
+        const int rl = seg >> 3, cl = (seg & 7) * 8;
+        const int row = m0 + wm + rl, col = n0 + wn + cl;
+        const u32x4 w8 = *(const u32x4 *)(ot16 + rl * P16 + cl);
+        if (row >= M || col >= N) continue;
+        uint16_t *d = (uint16_t *)Y + (size_t)row * N + col;
+        if (col + 8 <= N) {
+          *(u32x4 *)d = w8;
+        } else {
+          for (int e = 0; e < N - col; ++e) d[e] = (uint16_t)(w8[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+      continue;
+    }
+    constexpr int P32 = 32 + 4;  // fp32 pitch of a staged 32-column block
+    float *ot = (float *)smem + cw * 32 * P32;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ot[(8 * (e >> 2) + 4 * h + (e & 3)) * P32 + l32] = acc[r][j][e];
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int seg = it * 64 + lane;
+        const int rl = seg >> 2, cl = (seg & 3) * 8;
+        const int row = m0 + wm + rl, col = n0 + wn + 32 * j + cl;
+        float v[8];
+        {
+          const float4_t x0 = *(const float4_t *)(ot + rl * P32 + cl);
+          const float4_t x1 = *(const float4_t *)(ot + rl * P32 + cl + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = x0[e];
+            v[4 + e] = x1[e];
+          }
+        }
+        if (row >= M || col >= N) continue;
+        const int nv = min(8, N - col);
+        const size_t idx = (size_t)row * N + col;
+        if (ksplit > 1) {
+          float *dst = part + (size_t)split * M * N + idx;
+          if (vec && nv == 8) {
+            ((float4_t *)dst)[0] = float4_t{v[0], v[1], v[2], v[3]};
+            ((float4_t *)dst)[1] = float4_t{v[4], v[5], v[6], v[7]};
+          } else {
+            for (int e = 0; e < nv; ++e) dst[e] = v[e];
+          }
+          continue;
+        }
+        if (bias) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int cc = min(col + e, N - 1);
+            if (bdt == SF_F32) v[e] += ((const float *)bias)[cc];
+            else if (bdt == SF_F16) v[e] += (float)((const f16 *)bias)[cc];
+            else v[e] += sf_bf16_to_f32(((const uint16_t *)bias)[cc]);
+          }
+        }
+        store_row8(v, nv, vec, y32, Y, ydt, idx);
+      }
     }
   }
 }
@@ -945,14 +950,14 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
     static_assert(G_BM == BM && G_BN == BN && G_BK == BK, "one tiling: one split choice");
 #define SF_GW_LAUNCH(XD, AS, GKV)                                                              \
   do {                                                                                       \
-    constexpr size_t lds = (size_t)G_STAGES * g_stage_bytes<GKV == 0 ? 2 : 1>();            \
+    constexpr size_t lds = (size_t)g_lds_bytes<GKV == 0 ? 2 : 1>();                         \
     static bool attr = false; /* raise the dynamic LDS limit once per variant */             \
     if (!attr) {                                                                             \
-      (void)hipFuncSetAttribute((const void *)k_q4_gemm_w<XD, AS, GKV>,                      \
+      (void)hipFuncSetAttribute((const void *)k_q4_gemm_ws<XD, AS, GKV>,                     \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
       attr = true;                                                                           \
     }                                                                                        \
-    k_q4_gemm_w<XD, AS, GKV><<<grid, G_THREADS, lds, s>>>(w, st, zt, x, y, y_dtype, y_f32,   \
+    k_q4_gemm_ws<XD, AS, GKV><<<grid, G_THREADS, lds, s>>>(w, st, zt, x, y, y_dtype, y_f32,  \
                                                           bias, bias_dtype, part, M, N, K,   \
                                                           L.G, group_size, ksplit,            \
                                                           steps_per_split, vec);              \
