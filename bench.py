@@ -760,6 +760,14 @@ def summarize_kernels(trace_csv: str, *pmc_csvs: str) -> dict:
             e["wave_cycles_waiting_frac"] = round(ctr["SQ_WAIT_INST_ANY"] / ctr["SQ_WAVE_CYCLES"], 4)
         if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in ctr:
             e["mfma_bf16_flop"] = int(ctr["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512)
+        if "SQ_VALU_MFMA_COEXEC_CYCLES" in ctr and ctr.get("SQ_VALU_MFMA_BUSY_CYCLES"):
+            e["mfma_cycles_with_valu_frac"] = round(
+                ctr["SQ_VALU_MFMA_COEXEC_CYCLES"] / ctr["SQ_VALU_MFMA_BUSY_CYCLES"], 4)
+        if ctr.get("SQ_WAVES"):
+            mix = {n[len("SQ_INSTS_"):].lower(): round(ctr[n] / ctr["SQ_WAVES"], 1)
+                   for n in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU") if n in ctr}
+            if mix:
+                e["instructions_per_wave"] = mix
         out[k] = e
     return out
 

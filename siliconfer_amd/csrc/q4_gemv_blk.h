@@ -347,11 +347,13 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     if constexpr (PRE == PRE_RMSNORM)
       if (wave < B) nrm.issue<true>((const float *)a.x + (size_t)wave * K, nullptr, K);
   }
-  // ---- the epilogue's operands, loaded now so that the epilogue waits on no
-  // round trip of its own: the addend of each output (when every output has a
-  // thread of its own: thread e stores output e) and the RoPE position
+  // ---- the epilogue's operands of the decoder's folded variants, loaded now
+  // so that the epilogue waits on no round trip of its own: the addend of each
+  // output (when every output has a thread of its own: thread e stores output
+  // e) and the RoPE position (the plain GEMV keeps its loads in the epilogue:
+  // the early form costs it about 2% on its own)
   const int n_out = B * T * 16;
-  const bool out_pre = n_out <= NT;
+  const bool out_pre = (PRE != PRE_NONE || ROPE) && n_out <= NT;
   float addend = 0.f;
   if (out_pre && tid < n_out && a.bias) {
     const int b = tid / (T * 16), row = n0 + tid - b * (T * 16);
