@@ -678,11 +678,13 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[r][j] = gp[r][j] = zero16;
-  // acc += s * partial, s the group's scale of the lane's column
-  auto fold = [&](const uint8_t *stage, int q) {
-    float sc[2];
+  // the group's scale of the lane's columns
+  auto scales = [&](const uint8_t *stage, int q, float (&sc)[2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) sc[j] = (float)*(const f16 *)(stage + s_lds[j] + q * 1024);
+  };
+  // acc += s * partial
+  auto fold = [&](const float (&sc)[2]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -690,55 +692,85 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[r][j][e] = fmaf(gp[r][j][e], sc[j], acc[r][j][e]);
   };
-  // one 16-k slice (open: the slice starts its group)
-  auto slice = [&](const uint8_t *stage, const uint8_t *bo, int kk, bool open) {
+  // a 16-k slice's operands, read one slice ahead of its MFMAs so that each
+  // wait on LDS covers reads issued a slice earlier
+  struct Ops {
     u32x4 a[2], b[2];
+  };
+  auto ld = [&](const uint8_t *stage, const uint8_t *bo, int kk, Ops &o) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) a[r] = *(const u32x4 *)(stage + ((rb0 + r) * 4 + kk) * G_FRAG + lane * 16);
+    for (int r = 0; r < 2; ++r) o.a[r] = *(const u32x4 *)(stage + ((rb0 + r) * 4 + kk) * G_FRAG + lane * 16);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = *(const u32x4 *)(bo + ((cb0 + j) * 4 + kk) * 1024 + lane * 16);
+    for (int j = 0; j < 2; ++j) o.b[j] = *(const u32x4 *)(bo + ((cb0 + j) * 4 + kk) * 1024 + lane * 16);
+  };
+  // one 16-k slice's MFMAs (open: the slice starts its group)
+  auto mm = [&](const Ops &o, bool open) {
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const float16_t cin = open ? zero16 : gp[r][j];
         if constexpr (BF)
-          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf_bitcast<bf16x8_t>(a[r]),
-                                                             sf_bitcast<bf16x8_t>(b[j]), cin, 0, 0, 0);
+          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf_bitcast<bf16x8_t>(o.a[r]),
+                                                             sf_bitcast<bf16x8_t>(o.b[j]), cin, 0, 0, 0);
         else
-          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sf_bitcast<half8_t>(a[r]),
-                                                            sf_bitcast<half8_t>(b[j]), cin, 0, 0, 0);
+          gp[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sf_bitcast<half8_t>(o.a[r]),
+                                                            sf_bitcast<half8_t>(o.b[j]), cin, 0, 0, 0);
       }
   };
-  // `iss` (the loads of a later step) runs after the second slice
+  // `iss` (the loads of a later step) runs after the second slice. A group
+  // that ends with a step is folded at the top of the next one, while that
+  // step's first operand reads are in flight (its partials are not written
+  // again before the next step's first MFMAs; its scales are read at once,
+  // before the stage can be refilled).
+  float pend_s[2] = {0.f, 0.f};
+  bool pending = false;
   auto math_step = [&](int step, auto &&iss) {
     const uint8_t *stage = smem + (step & 3) * SB;
     const uint8_t *bo = bops + (step & 1) * G_B_BYTES;
+    Ops o0, o1;
+    ld(stage, bo, 0, o0);
+    ld(stage, bo, 1, o1);
+    if (pending) fold(pend_s);
+    pending = false;
     if constexpr (GK == 1) {
-      slice(stage, bo, 0, true);
-      slice(stage, bo, 1, false);
+      mm(o0, true);
+      ld(stage, bo, 2, o0);
+      mm(o1, false);
       iss();
-      slice(stage, bo, 2, false);
-      slice(stage, bo, 3, false);
-      fold(stage, 0);
+      ld(stage, bo, 3, o1);
+      mm(o0, false);
+      mm(o1, false);
+      scales(stage, 0, pend_s);
+      pending = true;
     } else if constexpr (GK == 0) {
-      slice(stage, bo, 0, true);
-      slice(stage, bo, 1, false);
+      mm(o0, true);
+      ld(stage, bo, 2, o0);
+      mm(o1, false);
       iss();
-      fold(stage, 0);
-      slice(stage, bo, 2, true);
-      slice(stage, bo, 3, false);
-      fold(stage, 1);
+      ld(stage, bo, 3, o1);
+      float sa[2];
+      scales(stage, 0, sa);
+      fold(sa);
+      mm(o0, true);
+      mm(o1, false);
+      scales(stage, 1, pend_s);
+      pending = true;
     } else {
       const bool fresh = step % spg == 0 || step == s0;
       const bool last = (step + 1) % spg == 0 || step == s1 - 1;
-      if (fresh) slice(stage, bo, 0, true);
-      else slice(stage, bo, 0, false);
-      slice(stage, bo, 1, false);
+      if (fresh) mm(o0, true);
+      else mm(o0, false);
+      ld(stage, bo, 2, o0);
+      mm(o1, false);
       iss();
-      slice(stage, bo, 2, false);
-      slice(stage, bo, 3, false);
-      if (last) fold(stage, 0);
+      ld(stage, bo, 3, o1);
+      mm(o0, false);
+      mm(o1, false);
+      if (last) {
+        scales(stage, 0, pend_s);
+        pending = true;
+      }
     }
   };
 
@@ -788,6 +820,7 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // outputs without split or fp32 copy round in registers (bias added first)
   // and stage 16-bit values; the rest stage fp32 values, one 32-column block
   // at a time.
+  if (math && pending) fold(pend_s);  // the last group's fold
   SF_WAIT_VM(0);
   __syncthreads();
   if (!math) return;
