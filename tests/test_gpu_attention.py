@@ -129,6 +129,56 @@ def test_partial_cache_prefix(dev):
     assert_close(out.cpu().numpy(), ref, TOL, "prefix")
 
 
+@pytest.mark.parametrize("sdtype", [np.float16, np.float32])
+@pytest.mark.parametrize("T,S", [(1, 8), (31, 8), (100, 8), (520, 8), (1000, 32), (321, 1),
+                                 (700, 0)])
+def test_rows_past_length_never_read_into_the_result(dev, sdtype, T, S):
+    """The cache rows at and past the length T hold anything (here random codes
+    and NaN scales): the result equals the one over a cache whose rows past T
+    are zeros, bit for bit, on the host-length and the device-length paths. The
+    split kernel loads a wave's first tiles before the length is known, so these
+    rows are read and must be masked (S = 0: the default split count)."""
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    T_cap, B, H, KVH, D = 1024, 1, 14, 2, 64
+    rng = np.random.default_rng(T + S)
+    q, kc, ks, vc, vs = make_inputs(rng, B, H, KVH, D, T_cap, sdtype)
+    clean = [a.copy() for a in (kc, ks, vc, vs)]
+    dirty = [a.copy() for a in (kc, ks, vc, vs)]
+    for a in clean:
+        a[:, :, T:] = 0 if a.dtype == np.int8 else 1
+    for a in dirty:
+        if a.dtype == np.int8:
+            a[:, :, T:] = rng.integers(-127, 128, a[:, :, T:].shape, dtype=np.int8)
+        else:
+            a[:, :, T:] = np.nan
+    t = lambda a: torch.as_tensor(a).to(dev).contiguous()
+    st = torch.cuda.current_stream().cuda_stream
+    nsp = S if S > 0 else int(lib.sf_attn_default_splits_d(B, KVH, T_cap, D))
+    ws = torch.empty((max(lib.sf_attn_workspace_bytes(B, H, D, max(nsp, 2)), 256),),
+                     dtype=torch.uint8, device=dev)
+    T_dev = torch.tensor([T], dtype=torch.int32, device=dev)
+    outs = []
+    for kc_, ks_, vc_, vs_ in (clean, dirty):
+        kcd, ksd, vcd, vsd, qd = t(kc_), t(ks_), t(vc_), t(vs_), t(q)
+        args = (qd.data_ptr(), _lib.SF_F32, kcd.data_ptr(), ksd.data_ptr(), vcd.data_ptr(),
+                vsd.data_ptr(), _lib.dt(ksd))
+        host = attention_decode(qd, kcd, ksd, vcd, vsd, T=T, n_splits=S or None)
+        devo = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+        _lib.check(lib.sf_attn_decode_i8kv_dev(*args, devo.data_ptr(), _lib.SF_F32, ws.data_ptr(),
+                                               ws.numel(), B, H, KVH, T_dev.data_ptr(), 0, T_cap,
+                                               T_cap, D, float(D ** -0.5), nsp, st),
+                   "sf_attn_decode_i8kv_dev")
+        torch.cuda.synchronize()
+        outs.append((host.cpu(), devo.cpu()))
+    for i in range(2):
+        assert torch.isfinite(outs[1][i]).all()
+        assert torch.equal(outs[0][i], outs[1][i]), ("host", "device")[i]
+    ref = A.attention_decode(q, kc, ks.astype(np.float64), vc, vs.astype(np.float64), T=T)
+    assert_close(outs[1][1].numpy(), ref, TOL, f"device length T={T} S={nsp}")
+
+
 @pytest.mark.parametrize("D", [16, 128, 256])
 def test_head_dims(dev, D):
     rng = np.random.default_rng(D)
