@@ -124,6 +124,27 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
   __shared__ int bi_s[kThreads / 64];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = H >> 3;  // 16-byte chunks per row
+  const int n_waves = gridDim.x * (kThreads / 64);
+  const int gw = blockIdx.x * (kThreads / 64) + wave;
+  constexpr int RU = 4;   // rows per wave and pass
+  constexpr int CPL = 2;  // chunks per lane (H <= 1024 in one pass)
+  // a pass's rows: two passes in flight (the next pass's loads go out before
+  // this pass's arithmetic), the first before the activations' norm, which
+  // they do not depend on; nontemporal, the table is streamed once
+  u32x4 cb[2][RU][CPL];
+  auto load_rows = [&](int r0, u32x4 (&c)[RU][CPL]) {
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int row = min(r0 + u * n_waves, V - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int ch = min(lane + 64 * j, nch - 1);
+        c[u][j] = __builtin_nontemporal_load((const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8));
+      }
+    }
+  };
+  if (gw < V) load_rows(gw, cb[0]);
   if constexpr (NORM) {
     const float *xf = (const float *)x;
     const float inv = sf_row_inv_rms(xf, nullptr, H, eps);
@@ -132,24 +153,10 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
     for (int h = tid; h < H; h += kThreads) xs[h] = sf_load_as_f32<XDT>(x, h);
   }
   __syncthreads();
-  const int nch = H >> 3;  // 16-byte chunks per row
-  const int n_waves = gridDim.x * (kThreads / 64);
-  const int gw = blockIdx.x * (kThreads / 64) + wave;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
-  constexpr int RU = 4;   // rows in flight per wave
-  constexpr int CPL = 2;  // chunks per lane (H <= 1024 in one pass)
-  for (int r0 = gw; r0 < V; r0 += RU * n_waves) {
-    u32x4 c[RU][CPL];
-#pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const int row = min(r0 + u * n_waves, V - 1);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int ch = min(lane + 64 * j, nch - 1);
-        c[u][j] = *(const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8);
-      }
-    }
+  // one pass: the RU rows r0 + u * n_waves from c
+  auto pass = [&](int r0, const u32x4 (&c)[RU][CPL]) {
     // rows longer than CPL * 64 chunks: the rest, one pass at a time
     float acc[RU];
 #pragma unroll
@@ -190,6 +197,14 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
         }
       }
     }
+  };
+  const int step = RU * n_waves;
+  for (int r0 = gw; r0 < V; r0 += 2 * step) {  // two passes per turn: static buffers
+    if (r0 + step < V) load_rows(r0 + step, cb[1]);
+    pass(r0, cb[0]);
+    if (r0 + step >= V) break;
+    if (r0 + 2 * step < V) load_rows(r0 + 2 * step, cb[0]);
+    pass(r0 + step, cb[1]);
   }
   if (lane == 0) {
     bv_s[wave] = best;
