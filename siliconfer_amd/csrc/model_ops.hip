@@ -176,7 +176,7 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
       }
       const int row = r0 + u * n_waves;
       for (int ch = lane + 64 * CPL; ch < nch; ch += 64) {
-        const u32x4 q = *(const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8);
+        const u32x4 q = __builtin_nontemporal_load((const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           a = fmaf(sf_bitcast<float>(q[e] << 16), xs[ch * 8 + 2 * e], a);
@@ -315,7 +315,7 @@ k_lm_head_rows(const uint16_t *__restrict__ w, const void *__restrict__ x,
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int ch = min(lane + 64 * j, nch - 1);
-        c[u][j] = *(const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8);
+        c[u][j] = __builtin_nontemporal_load((const u32x4 *)(w + (size_t)row * H + (size_t)ch * 8));
       }
     }
 #pragma unroll
@@ -337,7 +337,8 @@ k_lm_head_rows(const uint16_t *__restrict__ w, const void *__restrict__ x,
           }
         }
         for (int ch = lane + 64 * CPL; ch < nch; ch += 64) {
-          const u32x4 qv = *(const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8);
+          const u32x4 qv =
+              __builtin_nontemporal_load((const u32x4 *)(w + (size_t)min(row, V - 1) * H + (size_t)ch * 8));
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             a = fmaf(sf_bitcast<float>(qv[e] << 16), sf_load_as_f32<XDT>(xb, ch * 8 + 2 * e), a);
