@@ -950,7 +950,9 @@ namespace {
 // Merge launch of a split-T call: one lane per output element (row bh, dim d),
 // the splits in order with the rule of split_merge.h. Up to kMergeLoadSplits
 // splits, every load of the element goes out before the first use; longer
-// rows take M in a first pass.
+// rows take M in a first pass, then the sums in chunks of kMergeLoadSplits
+// splits whose loads go out together (a loop of one split per trip leaves
+// each load's latency exposed).
 constexpr int kMergeLoadSplits = 64;
 constexpr int kMergeThreads = 64;
 
@@ -985,15 +987,32 @@ k_attn_merge(const float *__restrict__ acc, const float *__restrict__ ml, void *
         L = fmaf(mv[j].y, w, L);
         v = fmaf(av[j], w, v);
       }
-  } else {
+  } else {  // chunks of C splits, each chunk's loads in flight together; sums in split order
     float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, mlr[s].x);
+    for (int s0 = 0; s0 < S; s0 += C) {
+      float mc[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j) mc[j] = s0 + j < S ? mlr[s0 + j].x : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < C; ++j) M = fmaxf(M, mc[j]);
+    }
     const float mref = sf_merge_mref(M);
-    for (int s = 0; s < S; ++s) {
-      const float2_t p = mlr[s];
-      const float w = sf_merge_weight(p.x, mref);
-      L = fmaf(p.y, w, L);
-      v = fmaf(ar[(size_t)s * D], w, v);
+    for (int s0 = 0; s0 < S; s0 += C) {
+      float2_t mv[C];
+      float av[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (s0 + j < S) {
+          mv[j] = mlr[s0 + j];
+          av[j] = ar[(size_t)(s0 + j) * D];
+        }
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (s0 + j < S) {
+          const float w = sf_merge_weight(mv[j].x, mref);
+          L = fmaf(mv[j].y, w, L);
+          v = fmaf(av[j], w, v);
+        }
     }
   }
   const float r = sf_merge_finish(L, v);
