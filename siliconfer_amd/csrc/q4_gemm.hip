@@ -14,8 +14,9 @@
 //    of 128): every operand byte (X fragments, the blob's W units, scales,
 //    zero-points) goes straight into LDS with buffer / global loads ... lds,
 //    four stages deep; four convert waves turn the next step's codes into
-//    the exact integers q - z as MFMA B operands in LDS while four math waves
-//    run the MFMAs and the per-group folds (described above the kernel).
+//    the exact integers q - z as MFMA B operands in LDS while eight math
+//    waves run the MFMAs and the per-group folds (described above the
+//    kernel).
 //  * k_q4_gemm (fp32 activations and the other multiples of 32): staging
 //    threads dequantize the W tile once into LDS as the integers q - z (exact
 //    in fp16 and bf16); fp32 activations are split into bf16 high and low
@@ -503,25 +504,29 @@ k_splitk_reduce(const float *__restrict__ part, void *__restrict__ Y, int ydt, f
 //    kk / 2).
 //  * the scale rows (16 cells of 8 fp16) and zero-point rows (16 cells of 8
 //    nibbles) of the step's groups.
-// The waves split by kind of work, one of each kind per SIMD, so that one
-// wave's MFMAs run beside the other's VALU work (with every wave doing both,
-// the per-step barrier keeps the two waves of a SIMD in the same phase and
-// the two kinds of work take turns):
-//  * waves 0..3 (math): rows 64 (w / 2) .. + 63 and columns 64 (w % 2) ..
-//    + 63 as 2 x 2 v_mfma_f32_32x32x16 tiles; each group's fp32 partial is
+// The waves split by kind of work, two math waves and one convert wave per
+// SIMD (waves w, w + 4 and w + 8 share one), so that MFMAs run beside the
+// VALU work (with every wave doing both, the per-step barrier keeps the waves
+// of a SIMD in the same phase and the two kinds of work take turns), and one
+// math wave's MFMAs fill the other's waits on LDS and on its fold:
+//  * waves 0..7 (math): rows 32 (w / 2) .. + 31 and columns 64 (w % 2) ..
+//    + 63 as 1 x 2 v_mfma_f32_32x32x16 tiles; each group's fp32 partial is
 //    folded into the result with its fp16 scale once per group (the
 //    reference's grouping, q4_gemv.cpp:136);
-//  * waves 4..7 (convert): during step s, wave 4 + c turns the codes of
+//  * waves 8..11 (convert): during step s, wave 8 + c turns the codes of
 //    column block c (32 columns) of step s + 1 into the exact integers q - z
 //    as bf16 or fp16 MFMA B operands (lane order) in one of two LDS operand
 //    buffers, which the math waves read in step s + 1.
 // Each wave's loads per step are a fixed count (math wave w: X fragments
-// 4 w .. + 3 and, for w < groups per step, that group's scale row; convert
-// wave 4 + c: W units 2 c, 2 c + 1 and, with zero-points and c < groups per
-// step, that group's zero-point row), so each wait is an exact s_waitcnt
-// vmcnt: a math wave waits for its loads of step s at the top of step s, a
-// convert wave for its loads of step s + 1.
-constexpr int G_BM = 128, G_BN = 128, G_BK = 64, G_THREADS = 512, G_STAGES = 4;
+// 4 (w / 2) + 2 (w % 2), + 1 and, for w < groups per step, that group's
+// scale row; convert wave 8 + c: W units 2 c, 2 c + 1 and, with zero-points
+// and c < groups per step, that group's zero-point row), so each wait is an
+// exact s_waitcnt vmcnt: a math wave waits for its loads of step s at the top
+// of step s, a convert wave for its loads of step s + 1.
+constexpr int G_BM = 128, G_BN = 128, G_BK = 64, G_STAGES = 4;
+constexpr int G_MATH = 8, G_THREADS = (G_MATH + 4) * 64;  // math waves, then 4 convert waves
+constexpr int G_XL = 16 / G_MATH;               // X fragments a math wave loads per step
+constexpr int G_MR = 4 * 4 / G_MATH / 2;        // 32-row blocks per math wave (2 column blocks each)
 constexpr int G_FRAG = 1024;                    // one A fragment (32 rows x 16 k)
 constexpr int G_X_BYTES = 16 * G_FRAG;          // a step's X
 constexpr int G_W_OFF = G_X_BYTES, G_W_BYTES = 8 * 1024;  // the tile's 8 units
@@ -585,8 +590,8 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool math = wave < 4;
-  const int cw = wave & 3;                          // index among the waves of its kind
+  const bool math = wave < G_MATH;
+  const int cw = math ? wave : wave - G_MATH;       // index among the waves of its kind
   const int l32 = lane & 31, h = lane >> 5;
   const int m0 = blockIdx.y * G_BM, n0 = blockIdx.x * G_BN;
   const int split = blockIdx.z;
@@ -599,7 +604,8 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
 
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)X, 0, M * K * 2, 0x00020000);
-  const int mrow = m0 + cw * 32 + l32;  // math wave cw loads row block cw's fragments
+  // math wave cw loads row block cw / 2's fragments G_XL (cw % 2) ..
+  const int mrow = m0 + (cw >> 1) * 32 + l32;
   const bool mrow_ok = mrow < M;
   const bool extra = math ? cw < NG : (ASYM && cw < NG);
   const int cell = min((n0 >> 3) + (lane & 15), ncells - 1);  // lanes 16.. repeat lane 15's row
@@ -608,13 +614,14 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
     uint8_t *stage = smem + (step & 3) * SB;
     if (math) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int i = 0; i < G_XL; ++i) {
+        const int f = G_XL * (cw & 1) + i;
         const int k = sc * G_BK + f * 16 + 8 * h;
         // past the resource (reads zero) unless in range; a select, not a branch
         const uint32_t in = ((uint32_t)mrow * (uint32_t)K + (uint32_t)k) * 2u;
         const uint32_t keep = 0u - (uint32_t)(mrow_ok && k < K);
         const uint32_t off = (in & keep) | (0x80000000u & ~keep);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (4 * cw + f) * G_FRAG), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (4 * (cw >> 1) + f) * G_FRAG), 16,
                                                  off, 0, 0, 0);
       }
     } else {
@@ -662,8 +669,8 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
     }
   };
 
-  // ---- math waves: row blocks 2 (cw / 2) + r, column blocks 2 (cw % 2) + j
-  const int rb0 = 2 * (cw >> 1), cb0 = 2 * (cw & 1);
+  // ---- math waves: row blocks G_MR (cw / 2) + r, column blocks 2 (cw % 2) + j
+  const int rb0 = G_MR * (cw >> 1), cb0 = 2 * (cw & 1);
   const int wn = 32 * cb0;
   int s_lds[2];
 #pragma unroll
@@ -673,9 +680,9 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   }
   const float16_t zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                             0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float16_t acc[2][2], gp[2][2];
+  float16_t acc[G_MR][2], gp[G_MR][2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < G_MR; ++r)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[r][j] = gp[r][j] = zero16;
   // the group's scale of the lane's columns
@@ -686,7 +693,7 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // acc += s * partial
   auto fold = [&](const float (&sc)[2]) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < G_MR; ++r)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -695,18 +702,18 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // a 16-k slice's operands, read one slice ahead of its MFMAs so that each
   // wait on LDS covers reads issued a slice earlier
   struct Ops {
-    u32x4 a[2], b[2];
+    u32x4 a[G_MR], b[2];
   };
   auto ld = [&](const uint8_t *stage, const uint8_t *bo, int kk, Ops &o) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) o.a[r] = *(const u32x4 *)(stage + ((rb0 + r) * 4 + kk) * G_FRAG + lane * 16);
+    for (int r = 0; r < G_MR; ++r) o.a[r] = *(const u32x4 *)(stage + ((rb0 + r) * 4 + kk) * G_FRAG + lane * 16);
 #pragma unroll
     for (int j = 0; j < 2; ++j) o.b[j] = *(const u32x4 *)(bo + ((cb0 + j) * 4 + kk) * 1024 + lane * 16);
   };
   // one 16-k slice's MFMAs (open: the slice starts its group)
   auto mm = [&](const Ops &o, bool open) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < G_MR; ++r)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const float16_t cin = open ? zero16 : gp[r][j];
@@ -797,8 +804,8 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
         const int step = s + u;
         if (step >= s1) break;
         if (math) {
-          if (extra) SF_WAIT_VM(10);
-          else SF_WAIT_VM(8);
+          if (extra) SF_WAIT_VM(2 * (G_XL + 1));
+          else SF_WAIT_VM(2 * G_XL);
         } else {
           if (extra) SF_WAIT_VM(3);
           else SF_WAIT_VM(2);
@@ -825,7 +832,7 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   __syncthreads();
   if (!math) return;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
+  for (int r = 0; r < G_MR; ++r) {
     const int wm = 32 * (rb0 + r);
     if (ksplit == 1 && !y32 && Y && vec && (ydt == SF_BF16 || ydt == SF_F16)) {
       constexpr int P16 = 64 + 8;  // halfword pitch of a staged row
