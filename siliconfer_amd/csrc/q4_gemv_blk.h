@@ -58,6 +58,7 @@
 //    saves.
 #pragma once
 #include <stdlib.h>
+#include <type_traits>
 
 #include "sf_common.h"
 #include "split_merge.h"
@@ -584,11 +585,36 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
       for (int r = 0; r < 4; ++r) red[(wave * 8 + 4 * kg + r) * (T * 16) + t * 16 + nl] = acc[t][r];
   }
   __syncthreads();
+  // one output's partials, summed in wave order: for the wave counts the
+  // plans use, all the reads go out before the first add (a loop over the
+  // runtime count leaves the compiler's remainder iterations each waiting on
+  // its read; reading a fixed maximum of slots instead measured slower)
+  auto wave_sum = [&](int idx) {
+    float v = 0.f;
+    auto sum_n = [&](auto n) {
+      constexpr int N = decltype(n)::value;
+      float pv[N];
+#pragma unroll
+      for (int wi = 0; wi < N; ++wi) pv[wi] = red[wi * 8 * (T * 16) + idx];
+#pragma unroll
+      for (int wi = 0; wi < N; ++wi) v += pv[wi];
+    };
+    switch (nw) {  // wave-uniform
+      case 7: sum_n(std::integral_constant<int, 7>{}); break;
+      case 8: sum_n(std::integral_constant<int, 8>{}); break;
+      case 10: sum_n(std::integral_constant<int, 10>{}); break;
+      case 11: sum_n(std::integral_constant<int, 11>{}); break;
+      case 14: sum_n(std::integral_constant<int, 14>{}); break;
+      case 16: sum_n(std::integral_constant<int, 16>{}); break;
+      default:
+        for (int wi = 0; wi < nw; ++wi) v += red[wi * 8 * (T * 16) + idx];
+    }
+    return v;
+  };
   if constexpr (ROPE) {
     float *hv = red + nw * 8 * (T * 16);  // the head's 64 outputs, bias added
     if (tid < 64) {  // B = 1, 64 outputs: out_pre holds
-      float v = 0.f;
-      for (int wi = 0; wi < nw; ++wi) v += red[(wi * 8) * (T * 16) + tid];
+      float v = wave_sum(tid);
       if (a.bias) v += addend;
       hv[tid] = v;
     }
@@ -600,8 +626,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     const int b = e / (T * 16), c = e - b * (T * 16);
     const int row = n0 + c;
     if (row >= a.N) continue;
-    float v = 0.f;
-    for (int wi = 0; wi < nw; ++wi) v += red[(wi * 8 + b) * (T * 16) + c];
+    float v = wave_sum(b * (T * 16) + c);
     if (out_pre) {
       if (a.bias) v += addend;
       store_sum(a.y, a.ydt, a.y32, (size_t)b * a.N + row, v);
