@@ -101,6 +101,29 @@ __device__ __forceinline__ float bias_value(const void *bias, int bdt, const flo
   return sf_bf16_to_f32(((const uint16_t *)bias)[row]);
 }
 
+// The addend's raw bits, loaded early without being used: two 16-bit loads at
+// an address chosen without a branch (fp32: its low and high halves; 16-bit
+// types: the value twice), so that no conversion, and no wait for this load
+// or for any load issued before it, sits between here and the epilogue.
+struct AddendBits {
+  uint32_t lo = 0, hi = 0;
+};
+__device__ __forceinline__ AddendBits addend_load(const void *bias, int bdt, const float *y32, size_t idx,
+                                                  int row) {
+  const bool res = bias == y32, wide = res || bdt == SF_F32;
+  const char *p = res ? (const char *)(y32 + idx) : (const char *)bias + (size_t)row * (wide ? 4 : 2);
+  AddendBits r;
+  r.lo = *(const uint16_t *)p;
+  r.hi = *(const uint16_t *)(p + (wide ? 2 : 0));
+  return r;
+}
+__device__ __forceinline__ float addend_value(AddendBits r, const void *bias, int bdt, const float *y32) {
+  asm volatile("" : "+v"(r.lo), "+v"(r.hi));  // converted here, at the point of use
+  if (bias == y32 || bdt == SF_F32) return sf_bitcast<float>(r.lo | (r.hi << 16));
+  if (bdt == SF_F16) return (float)sf_bitcast<f16>((uint16_t)r.lo);
+  return sf_bf16_to_f32((uint16_t)r.lo);
+}
+
 // Stores v (its addend already added) to y32 and / or y.
 __device__ __forceinline__ void store_sum(void *y, int ydt, float *y32, size_t idx, float v) {
   if (y32) y32[idx] = v;
@@ -355,10 +378,10 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   // the early form costs it about 2% on its own)
   const int n_out = B * T * 16;
   const bool out_pre = (PRE != PRE_NONE || ROPE) && n_out <= NT;
-  float addend = 0.f;
+  AddendBits addend;
   if (out_pre && tid < n_out && a.bias) {
     const int b = tid / (T * 16), row = n0 + tid - b * (T * 16);
-    if (row < a.N) addend = bias_value(a.bias, a.bdt, a.y32, (size_t)b * a.N + row, row);
+    if (row < a.N) addend = addend_load(a.bias, a.bdt, a.y32, (size_t)b * a.N + row, row);
   }
   int rpos = 0;
   if constexpr (ROPE) rpos = *pos_dev;
@@ -615,7 +638,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     float *hv = red + nw * 8 * (T * 16);  // the head's 64 outputs, bias added
     if (tid < 64) {  // B = 1, 64 outputs: out_pre holds
       float v = wave_sum(tid);
-      if (a.bias) v += addend;
+      if (a.bias) v += addend_value(addend, a.bias, a.bdt, a.y32);
       hv[tid] = v;
     }
     __syncthreads();
@@ -628,7 +651,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     if (row >= a.N) continue;
     float v = wave_sum(b * (T * 16) + c);
     if (out_pre) {
-      if (a.bias) v += addend;
+      if (a.bias) v += addend_value(addend, a.bias, a.bdt, a.y32);
       store_sum(a.y, a.ydt, a.y32, (size_t)b * a.N + row, v);
     } else {
       store_out(a.y, a.ydt, a.y32, a.bias, a.bdt, (size_t)b * a.N + row, row, v);
