@@ -485,7 +485,12 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   struct Tile {
     u32x4 k[2][KW / 4];  // K dwords of tokens hl and 16 + hl
     u32x4 v[VC];         // V chunks for the LDS stage
-    float ks[8], vs[8];  // scales of the lane's tokens T_g (as loaded; masked later)
+    // scale bits of the lane's tokens T_g as loaded (converted in compute, so
+    // that no use of a load waits on the tile's other loads and holds back
+    // the next tile's): token r's word is [r / 4][r % 4] (fp32 bits, or fp16 /
+    // bf16 in the low half), but with vscale fp16 pairs, tokens 4 h2 + 2 i and
+    // + 1 in the halves of word [h2][i]
+    u32x4 kw[2], vw[2];
   };
   auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
   // tile j's rows (clamped into the cache: a tile is loaded before the length
@@ -514,41 +519,56 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
         if constexpr (SDT == SF_F16) {
           const u32x2 a = *(const u32x2 *)((const f16 *)ks + row);
           const u32x2 c = *(const u32x2 *)((const f16 *)vs + row);
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const half2_t ka = sf_bitcast<half2_t>(a[i]), va = sf_bitcast<half2_t>(c[i]);
-            tl.ks[4 * h2 + 2 * i] = (float)ka.x;
-            tl.ks[4 * h2 + 2 * i + 1] = (float)ka.y;
-            tl.vs[4 * h2 + 2 * i] = (float)va.x;
-            tl.vs[4 * h2 + 2 * i + 1] = (float)va.y;
-          }
+          tl.kw[h2].x = a.x, tl.kw[h2].y = a.y;
+          tl.vw[h2].x = c.x, tl.vw[h2].y = c.y;
         } else {
-          const float4_t a = *(const float4_t *)((const float *)ks + row);
-          const float4_t c = *(const float4_t *)((const float *)vs + row);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            tl.ks[4 * h2 + i] = a[i];
-            tl.vs[4 * h2 + i] = c[i];
-          }
+          tl.kw[h2] = *(const u32x4 *)((const float *)ks + row);
+          tl.vw[h2] = *(const u32x4 *)((const float *)vs + row);
         }
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const size_t row = base + min(tb + tok_of(r), T_cap - 1);
-        tl.ks[r] = sf_load_as_f32<SDT>(ks, row);
-        tl.vs[r] = sf_load_as_f32<SDT>(vs, row);
+        if constexpr (SDT == SF_F32) {
+          tl.kw[r >> 2][r & 3] = ((const uint32_t *)ks)[row];
+          tl.vw[r >> 2][r & 3] = ((const uint32_t *)vs)[row];
+        } else {
+          tl.kw[r >> 2][r & 3] = ((const uint16_t *)ks)[row];
+          tl.vw[r >> 2][r & 3] = ((const uint16_t *)vs)[row];
+        }
       }
+    }
+  };
+  // scale r of a tile from its loaded bits
+  auto scale_of = [&](const u32x4 (&w4)[2], int r) {
+    if constexpr (SDT == SF_F32) {
+      return sf_bitcast<float>(w4[r >> 2][r & 3]);
+    } else {
+      // both candidates at constant indices, then a select
+      const uint32_t wp = w4[r >> 2][(r >> 1) & 1] >> (16 * (r & 1));
+      const uint32_t w1 = w4[r >> 2][r & 3];
+      const uint32_t w = SDT == SF_F16 && vscale ? wp : w1;
+      if constexpr (SDT == SF_F16) return (float)sf_bitcast<f16>((uint16_t)w);
+      else return sf_bf16_to_f32((uint16_t)w);
     }
   };
 
   // the wave's first tiles (those that start inside the cache), then the length
+  // The device-side length goes out as a vector load right behind the first
+  // tile's (a scalar load would be waited for by the next kernel-argument
+  // wait, before any tile goes out), so waiting for it leaves the later tiles
+  // in flight.
   Tile tl[NB];
+  int tdev = 0;
 #pragma unroll
-  for (int u = 0; u < NB; ++u)
+  for (int u = 0; u < NB; ++u) {
     if (32 * (j0 + jstep * u) < T_cap) load(j0 + jstep * u, tl[u]);
-  int Tv = T_dev ? *T_dev + T : T;
-  if (causal) Tv = (T_dev ? *T_dev : T) + b + 1;
+    if (u == 0 && T_dev) tdev = __hip_atomic_load(T_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("" : "+v"(tdev));  // read here, not right behind its load
+  int Tv = T_dev ? tdev + T : T;
+  if (causal) Tv = (T_dev ? tdev : T) + b + 1;
   Tv = max(0, min(Tv, T_cap));
   const int ntot = (Tv + 31) / 32;  // tiles holding tokens
   const int mine = j0 < ntot ? (ntot - j0 + jstep - 1) / jstep : 0;
@@ -561,6 +581,12 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
 
   auto compute = [&](int j, const Tile &tl) {
     const int tb = 32 * j;
+    float tks[8], tvs[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      tks[r] = scale_of(tl.kw, r);
+      tvs[r] = scale_of(tl.vw, r);
+    }
     // S^T for the two 16-token halves
     float4_t S[2];
 #pragma unroll
@@ -579,7 +605,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const bool valid = tb + tok_of(r) < Tv;
-      sc[r] = valid ? S[r >> 2][r & 3] * (tl.ks[r] * qscale) : -INFINITY;
+      sc[r] = valid ? S[r >> 2][r & 3] * (tks[r] * qscale) : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -595,7 +621,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
       ps += p;
       // masked tokens weigh exactly 0 (their scale may be any stale value)
-      const float pv = tb + tok_of(r) < Tv ? p * tl.vs[r] : 0.f;
+      const float pv = tb + tok_of(r) < Tv ? p * tvs[r] : 0.f;
       ph[r] = (f16)pv;
       pl[r] = (f16)(pv - (float)ph[r]);
     }
