@@ -300,6 +300,11 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   const int n0 = blockIdx.x * T * 16;
   const int B = a.B, K = a.K, G = a.G;
   const int KP = a.nblk * kUnitK;
+  // the RoPE position (device memory) as the first vector load, read only
+  // after the weights have gone out: a scalar load would be waited for by
+  // the next wait on the kernel's arguments, ahead of every weight load
+  int rpos_v = 0;
+  if constexpr (ROPE) rpos_v = __hip_atomic_load(pos_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int nt[T], ti[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -384,8 +389,7 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     if (row < a.N) addend = addend_load(a.bias, a.bdt, a.y32, (size_t)b * a.N + row, row);
   }
   int rpos = 0;
-  if constexpr (ROPE) rpos = *pos_dev;
-  const bool rope_ok = ROPE && rpos >= 0 && rpos < rope.T_cap && rpos < rope.max_pos;
+  bool rope_ok = false;
   SfRopeCS rcs{};
   __amdgpu_buffer_rsrc_t xrs;
   int xoff = 0;
@@ -458,8 +462,12 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   __builtin_amdgcn_sched_barrier(0);
   // the RoPE table rows at the position (after the weights: they need the
   // position's value, and arrive long before the epilogue)
-  if constexpr (ROPE)
+  if constexpr (ROPE) {
+    asm volatile("" : "+v"(rpos_v));  // read here, not right behind its load
+    rpos = rpos_v;
+    rope_ok = rpos >= 0 && rpos < rope.T_cap && rpos < rope.max_pos;
     if (c == 0 && tid < 64 && rope_ok) rcs = sf_rope_load_cs(rope, rpos);
+  }
 
   // ---- XL (first chunk): finish the producer, stage the activations, sync
   if constexpr (XL) if (c == 0) {
