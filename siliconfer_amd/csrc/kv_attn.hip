@@ -457,6 +457,11 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   constexpr int PITCH = D + 8;     // V tile row pitch in LDS, bytes
   constexpr bool QSPLIT = QDT != SF_F16;
   __shared__ __attribute__((aligned(16))) float smem[attn_mfma_smem_floats<D, NW>()];
+  // every argument fetched in one round at entry (left to itself the compiler
+  // splits the scalar loads around the first branches, one wait per round)
+  asm volatile("" ::"s"(q), "s"(kc), "s"(ks), "s"(vc), "s"(vs), "s"(part_acc), "s"(part_ml), "s"(out),
+               "s"(odt), "s"(H), "s"(KVH), "s"(T), "s"(T_dev), "s"(causal), "s"(T_cap), "s"(qscale),
+               "s"(n_splits), "s"(vscale));
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = H / KVH;

@@ -173,6 +173,7 @@ struct BlkArgs {
   float eps;
   const float *mml;   // PRE_MERGE: split (m, l) pairs (x is the split acc)
   int ms, md;         // PRE_MERGE: splits, head_dim
+  int nt;             // threads per workgroup (the launch's block size)
 };
 
 // Activations staged per thread in XL mode, in pieces of 8 consecutive k of one
@@ -293,8 +294,17 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   constexpr int XPRE = XL ? 0 : (XR == BPW ? BPW : XR - 1);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float inv_s[8];
-
-  const int tid = threadIdx.x, lane = tid & 63, NT = blockDim.x, nw = NT >> 6;
+  // Every argument the prologue reads, fetched in one round at entry: left to
+  // itself the compiler splits these scalar loads around the prologue's first
+  // branches, and each round is a wait on the kernel-argument memory before
+  // any activation or weight load goes out.
+  asm volatile("" ::"s"(a.w), "s"(a.st), "s"(a.zt), "s"(a.x), "s"(a.y), "s"(a.y32), "s"(a.bias),
+               "s"(a.pre_w), "s"(a.mml), "s"(a.B), "s"(a.N), "s"(a.K), "s"(a.G), "s"(a.nblk),
+               "s"(a.ntiles), "s"(a.gmul), "s"(a.uq), "s"(a.ur), "s"(a.xp), "s"(a.bdt), "s"(a.ydt),
+               "s"(a.ms), "s"(a.md), "s"(a.eps), "s"(a.nt));
+  // the thread count from the arguments (blockDim is a further read of the
+  // dispatch's own arguments)
+  const int tid = threadIdx.x, lane = tid & 63, NT = a.nt, nw = NT >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * T * 16;
@@ -783,7 +793,8 @@ void launch_cfg(const BlkPlan &p, const GemvArgs &g, const float *pre_w, float e
   }
   const uint32_t gmul = (uint32_t)(((1ull << 30) + g.g - 1) / g.g);
   const BlkArgs ba{g.w, g.st, g.zt, g.x, g.y, g.ydt, g.y32, g.bias, g.bdt, g.B, g.N, g.K, g.G, g.g,
-                   p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps, g.mml, g.ms, g.md};
+                   p.nblk, p.ntiles, gmul, p.uq, p.ur, p.xp, pre_w, eps, g.mml, g.ms, g.md,
+                   p.nw * 64};
   const SfRopeAppend ra = rope ? *rope : SfRopeAppend{};
   k_q4_gemv_blk<X, A, GK, T, BPW, XL, PRE, ROPE, KC><<<p.grid, p.nw * 64, p.lds, g.s>>>(ba, ra, pos_dev);
 }
