@@ -990,6 +990,8 @@ constexpr int kMergeThreads = 64;
 __global__ void __launch_bounds__(kMergeThreads)
 k_attn_merge(const float *__restrict__ acc, const float *__restrict__ ml, void *__restrict__ out,
              int odt, int rows, int D, int S) {
+  // every argument fetched in one round at entry (the compiler would split them)
+  asm volatile("" ::"s"(acc), "s"(ml), "s"(out), "s"(odt), "s"(rows), "s"(D), "s"(S));
   constexpr int C = kMergeLoadSplits;
   const int e = blockIdx.x * kMergeThreads + threadIdx.x;
   if (e >= rows * D) return;
