@@ -440,6 +440,31 @@ constexpr int attn_mfma_smem_floats() {
 // path) has arrived; rows are clamped into the cache and tokens at or past the
 // length are masked. Tiles start on 32-token boundaries, so when T_cap % 4 ==
 // 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
+// max / sum of a value and its partner 16 or 32 lanes away (the lane xor 16 /
+// xor 32), with gfx950's row-swapping permutes: each returns the value and
+// its partner in some order, both register-only (a shuffle is an LDS round
+// trip); max and + of the same two operands give the shuffle's bits.
+__device__ __forceinline__ float2_t swap16_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
+  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
+}
+__device__ __forceinline__ float2_t swap32_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
+  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
+}
+__device__ __forceinline__ float max_x16_x32(float v) {
+  float2_t p = swap16_pair(v);
+  v = fmaxf(p.x, p.y);
+  p = swap32_pair(v);
+  return fmaxf(p.x, p.y);
+}
+__device__ __forceinline__ float sum_x16_x32(float v) {
+  float2_t p = swap16_pair(v);
+  v = p.x + p.y;
+  p = swap32_pair(v);
+  return p.x + p.y;
+}
+
 template <int QDT, int SDT, int D, int NW, int NB>
 __global__ void __launch_bounds__(NW * 64)
 k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
@@ -613,8 +638,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       sc[r] = valid ? S[r >> 2][r & 3] * (tks[r] * qscale) : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_x16_x32(mx);
     const float m_new = fmaxf(m, mx);
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;
     const float c = __builtin_amdgcn_exp2f(m - m_ref);  // exp2(-inf) = 0
@@ -664,8 +688,7 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
       }
     }
   }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  lsum = sum_x16_x32(lsum);
 
   // ---- merge the 4 wave states (LDS)
   float *ms = smem + NW * 32 * PITCH / 4;  // [NW][16]
