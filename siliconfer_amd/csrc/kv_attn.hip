@@ -440,28 +440,17 @@ constexpr int attn_mfma_smem_floats() {
 // path) has arrived; rows are clamped into the cache and tokens at or past the
 // length are masked. Tiles start on 32-token boundaries, so when T_cap % 4 ==
 // 0 (vscale) a lane's 8 scales are two aligned 4-token loads.
-// max / sum of a value and its partner 16 or 32 lanes away (the lane xor 16 /
-// xor 32), with gfx950's row-swapping permutes: each returns the value and
-// its partner in some order, both register-only (a shuffle is an LDS round
-// trip); max and + of the same two operands give the shuffle's bits.
-__device__ __forceinline__ float2_t swap16_pair(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
-  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
-}
-__device__ __forceinline__ float2_t swap32_pair(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
-  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
-}
+// max / sum of a value and its partners 16 and 32 lanes away (see sf_swap16_pair)
 __device__ __forceinline__ float max_x16_x32(float v) {
-  float2_t p = swap16_pair(v);
+  float2_t p = sf_swap16_pair(v);
   v = fmaxf(p.x, p.y);
-  p = swap32_pair(v);
+  p = sf_swap32_pair(v);
   return fmaxf(p.x, p.y);
 }
 __device__ __forceinline__ float sum_x16_x32(float v) {
-  float2_t p = swap16_pair(v);
+  float2_t p = sf_swap16_pair(v);
   v = p.x + p.y;
-  p = swap32_pair(v);
+  p = sf_swap32_pair(v);
   return p.x + p.y;
 }
 

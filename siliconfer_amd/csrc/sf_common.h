@@ -165,6 +165,19 @@ __device__ __forceinline__ float sf_dpp(float v) {
   return sf_bitcast<float>(__builtin_amdgcn_update_dpp(0, sf_bitcast<int>(v), CTRL, 0xF, 0xF, false));
 }
 
+// A value and its partner 16 (32) lanes away, lane xor 16 (xor 32), with
+// gfx950's row-swapping permutes: the pair comes back in some order, both
+// register-only (a shuffle is an LDS round trip). max and + of the same two
+// operands give the shuffle-based step's bits. All 64 lanes must be active.
+__device__ __forceinline__ float2_t sf_swap16_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
+  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
+}
+__device__ __forceinline__ float2_t sf_swap32_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(sf_bitcast<uint32_t>(v), sf_bitcast<uint32_t>(v), false, false);
+  return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the same bits (each step
 // adds a value and its butterfly partner, and fp addition commutes).
 __device__ __forceinline__ float sf_wave_sum(float v) {
@@ -172,9 +185,10 @@ __device__ __forceinline__ float sf_wave_sum(float v) {
   v += sf_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += sf_dpp<0x141>(v);  // row_half_mirror
   v += sf_dpp<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  float2_t p = sf_swap16_pair(v);
+  v = p.x + p.y;
+  p = sf_swap32_pair(v);
+  return p.x + p.y;
 }
 
 // 1 / sqrt(mean((x + delta)^2) + eps) over one row of H fp32 values, computed
@@ -282,9 +296,17 @@ struct SfRopeAppend {
   int scale_dtype, H, KVH, D, T_cap;
 };
 
+// Max over the 64 lanes of a wave (every lane gets it): the within-row steps
+// as DPP moves, the cross-row ones as permlane swaps. All lanes active.
 __device__ __forceinline__ float sf_wave_max(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, sf_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, sf_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, sf_dpp<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, sf_dpp<0x140>(v));  // row_mirror
+  float2_t p = sf_swap16_pair(v);
+  v = fmaxf(p.x, p.y);
+  p = sf_swap32_pair(v);
+  return fmaxf(p.x, p.y);
 }
 
 __device__ __forceinline__ void sf_store_dt(void *p, int dt, size_t i, float v) {
