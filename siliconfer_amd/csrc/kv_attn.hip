@@ -873,8 +873,7 @@ k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
       sc[r] = valid ? S[r >> 2][r & 3] * (tl.ks[r] * qscale) : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_x16_x32(mx);
     const float m_new = fmaxf(m, mx);
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;
     const float cf = __builtin_amdgcn_exp2f(m - m_ref);
@@ -926,8 +925,7 @@ k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
       }
     }
   }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  lsum = sum_x16_x32(lsum);
   if (c0 + hl >= ncol) return;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   const size_t o = qrow * D;

@@ -617,7 +617,10 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] += __shfl_xor(acc[t][r], 32, 64);
+      for (int r = 0; r < 4; ++r) {
+        const float2_t pr = sf_swap32_pair(acc[t][r]);  // the lane and lane ^ 32
+        acc[t][r] = pr.x + pr.y;
+      }
   }
   if (kg < 2) {
 #pragma unroll
