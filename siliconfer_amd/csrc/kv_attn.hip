@@ -735,16 +735,19 @@ int pow2_log2_at_least(int v) {
 // causal prefill attention, flash style on MFMA
 // ---------------------------------------------------------------------------
 // The prompt's query rows of one kv head are the (token, head) pairs
-// c = t * G + h; each wave owns 16 consecutive ones as the 16 MFMA columns
-// and walks the key tiles 0, 32, 64, ... up to the causal limit of its last
-// row, keeping each row's online softmax (base 2) as the decode kernel keeps
-// each head's: S^T = K Q^T (K codes -> exact fp16 as the A operand, the rows'
-// q as the B operand, fp16 hi + lo for fp32 / bf16 q), a key past a row's
-// own limit T0 + t + 1 weighs exactly 0, and O^T = V^T P^T takes P^T from the
-// S^T registers (V scale folded, hi + lo) and V^T from the wave's LDS stage
-// through ds_read_b64_tr_b8. Each row's result is final in its wave: no merge
-// across waves or workgroups, no barrier. Every K / V tile is read once per
-// wave (16 query rows), not once per query row.
+// c = t * G + h; a workgroup owns 16 consecutive ones as the 16 MFMA columns,
+// and its waves share the key tiles 0, 32, 64, ... up to the causal limit of
+// the last row round robin (wave w takes tiles w, w + NW, ...), each keeping
+// every row's online softmax (base 2) as the decode kernel keeps each head's:
+// S^T = K Q^T (K codes -> exact fp16 as the A operand, the rows' q as the B
+// operand, fp16 hi + lo for fp32 / bf16 q), a key past a row's own limit
+// T0 + t + 1 weighs exactly 0, and O^T = V^T P^T takes P^T from the S^T
+// registers (V scale folded, hi + lo) and V^T from the wave's LDS stage
+// through ds_read_b64_tr_b8. The wave states (m, l, O per row) merge through
+// LDS at the end with the decode kernel's rule. Workgroups go out longest
+// rows first, the kv heads interleaved, so the short early rows fill in
+// behind them. Every K / V tile is read once per workgroup (16 query rows),
+// not once per query row.
 constexpr int kPfWaves = 4;
 
 template <int QDT, int SDT, int D>
@@ -759,15 +762,18 @@ k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
   constexpr int KS = D / 32, DB = D / 16, KW = D / 16, VC = D / 32, PITCH = D + 8;
   constexpr bool QSPLIT = QDT != SF_F16;
   __shared__ __attribute__((aligned(16))) float smem[NW * 32 * PITCH / 4];
+  __shared__ __attribute__((aligned(16))) float os[NW * 16 * D];  // wave states: O
+  __shared__ float ms[NW * 16], ls[NW * 16];                     // and m, l per row
 
-  const int kvh = blockIdx.y;
+  const int kvh = (int)(blockIdx.x % (unsigned)KVH);
   const int G = H / KVH;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hl = lane & 15, g = lane >> 4;
   const int ncol = T_q * G;
-  const int c0 = (blockIdx.x * NW + wave) * 16;
-  if (c0 >= ncol) return;  // wave-uniform; nothing below waits on other waves
+  const int nblk = (ncol + 15) >> 4;
+  const int c0 = (nblk - 1 - (int)(blockIdx.x / (unsigned)KVH)) * 16;  // longest rows first
+  if (c0 < 0) return;  // workgroup-uniform (the host's grid has none past the rows)
   const int start = T0_dev ? *T0_dev : T0;
   const int c = min(c0 + hl, ncol - 1);  // columns past the rows repeat the last one (not stored)
   const int tq = c / G, hh = c - tq * G;
@@ -794,6 +800,7 @@ k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
     float ks[8], vs[8];
   };
   const int ntiles = (t1 + 31) / 32;
+  const int mine = wave < ntiles ? (ntiles - wave + NW - 1) / NW : 0;  // tiles wave + NW i
   auto tok_of = [&](int r) { return (r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4)); };
   auto load = [&](int j, Tile &tl) {
     const int tb = 32 * j;
@@ -914,31 +921,55 @@ k_attn_prefill_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc,
   Tile tl[NB];
 #pragma unroll
   for (int u = 0; u < NB; ++u)
-    if (u < ntiles) load(u, tl[u]);
-  for (int i0 = 0; i0 < ntiles; i0 += NB) {
+    if (u < mine) load(wave + NW * u, tl[u]);
+  for (int i0 = 0; i0 < mine; i0 += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int i = i0 + u;
-      if (i < ntiles) {
-        compute(i, tl[u]);
-        if (i + NB < ntiles) load(i + NB, tl[u]);
+      if (i < mine) {
+        compute(wave + NW * i, tl[u]);
+        if (i + NB < mine) load(wave + NW * (i + NB), tl[u]);
       }
     }
   }
   lsum = sum_x16_x32(lsum);
-  if (c0 + hl >= ncol) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  const size_t o = qrow * D;
+
+  // ---- merge the wave states (a wave without tiles holds m = -inf, l = 0, O = 0)
+  if (g == 0) {
+    ms[wave * 16 + hl] = m;
+    ls[wave * 16 + hl] = lsum;
+  }
 #pragma unroll
   for (int d = 0; d < DB; ++d)
+    *(float4_t *)(os + (wave * 16 + hl) * D + 16 * d + 4 * g) = O[d];
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * (D / 4); e += NW * 64) {
+    const int h = e / (D / 4), d4 = (e - h * (D / 4)) * 4;
+    const int col = c0 + h;
+    if (col >= ncol) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, ms[w * 16 + h]);
+    const float M_ref = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(ms[w * 16 + h] - M_ref);
+      L = fmaf(wt, ls[w * 16 + h], L);
+      a += *(const float4_t *)(os + (w * 16 + h) * D + d4) * wt;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int tq = col / G, hh = col - tq * G;
+    const size_t o = ((size_t)tq * H + (size_t)kvh * G + hh) * D + d4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float v = O[d][i] * inv;
-      const size_t idx = o + 16 * d + 4 * g + i;
-      if (odt == SF_F32) ((float *)out)[idx] = v;
-      else if (odt == SF_F16) ((f16 *)out)[idx] = (f16)v;
-      else ((uint16_t *)out)[idx] = sf_f32_to_bf16(v);
+      const float v = a[i] * inv;
+      if (odt == SF_F32) ((float *)out)[o + i] = v;
+      else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
+      else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
     }
+  }
 }
 
 }  // namespace
@@ -1306,9 +1337,10 @@ static int prefill_mfma_launch(const char *what, const void *q, int q_dtype, con
   const int vscale = T_cap % 4 == 0 && T_cap >= 4 && (uintptr_t)k_scales % sal == 0 &&
                      (uintptr_t)v_scales % sal == 0;
   const long long ncol = (long long)T_q * G;
-  const long long nblk = (ncol + 16 * kPfWaves - 1) / (16 * kPfWaves);
-  SF_REQUIRE(nblk <= 0x7fffffff, SF_EINVAL, "prefill of %d rows is too long", T_q);
-  dim3 grid((unsigned)nblk, KVH, 1);
+  const long long nblk = (ncol + 15) / 16;  // 16-row blocks; one workgroup per block and kv head
+  SF_REQUIRE(ncol <= 0x7fffffff && nblk * KVH <= 0x7fffffff, SF_EINVAL,
+             "prefill of %d rows is too long", T_q);
+  dim3 grid((unsigned)(nblk * KVH), 1, 1);
   hipStream_t st = (hipStream_t)stream;
 #define SF_PF_LAUNCH(QD, SD, DD)                                                               \
   k_attn_prefill_mfma<QD, SD, DD><<<grid, kPfWaves * 64, 0, st>>>(                            \
