@@ -155,6 +155,20 @@ int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtyp
                const void *bias, int bias_dtype, int M, int N, int K, int group_size,
                int has_zeros, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The prefill GEMM with its K-split partials left for the next op (no
+ * counterpart in the reference, whose q4_gemm returns Y; here the decoder's
+ * prompt path folds the residual delta into the RMSNorm that follows).
+ * sf_q4_gemm_splits: the number of K splits sf_q4_gemm runs for this shape
+ * (1: unsplit; 0: invalid shape or a group size that is not a multiple of 32).
+ * sf_q4_gemm_partials: for a shape with 2+ splits, writes split s's fp32
+ * partial of Y[m, n] at workspace[s * M * N + m * N + n] and launches nothing
+ * else; SF_EINVAL for an unsplit shape. The partials summed in split order
+ * from 0 are the sums sf_q4_gemm's own reduce forms. */
+int sf_q4_gemm_splits(int M, int N, int K, int group_size);
+int sf_q4_gemm_partials(const void *blob, const void *x, int x_dtype, int M, int N, int K,
+                        int group_size, int has_zeros, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
 /* ---- int8 KV cache ----------------------------------------------------------
  * Quantize T_new new tokens and write them at positions [T_off, T_off+T_new)
  * of a preallocated cache. Replaces quantize_kv + the concatenation in
@@ -289,6 +303,15 @@ int sf_embed(const int32_t *ids, const void *table, int table_dtype, float *out,
  * out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w. */
 int sf_rmsnorm(float *x, const float *delta, const void *w, int w_dtype, void *out, int out_dtype,
                int rows, int H, float eps, void *stream);
+
+/* sf_rmsnorm with delta given as the n_parts K-split partials of
+ * sf_q4_gemm_partials for rows x H outputs (partial s at
+ * part[s * rows * H + r * H + h]): delta = the partials summed in split order
+ * from 0. x and out get the bits of sf_q4_gemm into a delta buffer followed
+ * by sf_rmsnorm(x, delta), with one launch less (the same layers.py:14-21,
+ * 160-162). */
+int sf_rmsnorm_partials(float *x, const float *part, int n_parts, const void *w, int w_dtype,
+                        void *out, int out_dtype, int rows, int H, float eps, void *stream);
 
 /* RoPE (layers.py:58-66, rotate-half) of the q and k heads of the fused q|k|v
  * projection rows qkv [rows][(H + 2 KVH) * D] at positions pos0 + r, then the

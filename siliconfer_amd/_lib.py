@@ -48,6 +48,9 @@ _SIGS = {
     "sf_q4_gemm_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
     "sf_q4_gemm": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i,
                           _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),
+    "sf_q4_gemm_splits": (_c_i, [_c_i, _c_i, _c_i, _c_i]),
+    "sf_q4_gemm_partials": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz,
+                                   _c_p]),
     "sf_kv_quant_append": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i,
                                   _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "sf_attn_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
@@ -75,6 +78,8 @@ _SIGS = {
                                         _c_i, _c_p]),
     "sf_embed": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p]),
     "sf_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_f, _c_p]),
+    "sf_rmsnorm_partials": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_f,
+                                   _c_p]),
     "sf_rope_kv_append": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p,
                                  _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_i, _c_p]),
     "sf_silu_mul": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_i, _c_p]),

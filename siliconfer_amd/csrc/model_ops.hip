@@ -67,6 +67,46 @@ k_rmsnorm(float *__restrict__ x, const float *__restrict__ delta, const void *__
   }
 }
 
+// k_rmsnorm with the residual delta as K-split partials (S of them, MN apart):
+// each element's delta summed in split order from 0 (the GEMM reduce's sum)
+// goes into x first; after the barrier the row's norm reads x as k_rmsnorm
+// reads x + delta, so x and out get k_rmsnorm's bits.
+__global__ void __launch_bounds__(kThreads)
+k_rmsnorm_parts(float *__restrict__ x, const float *__restrict__ part, int S, size_t MN,
+                const void *__restrict__ w, int wdt, void *__restrict__ out, int odt, int H,
+                float eps) {
+  const size_t r0 = (size_t)blockIdx.x * H;
+  constexpr int C = 8;  // partials whose loads go out together (a split GEMM has at most 8)
+  if ((H & 3) == 0 && (((uintptr_t)x | (uintptr_t)part) & 15) == 0 && MN % 4 == 0) {
+    // 4 consecutive elements per thread, every load in flight before the sums
+    float4_t *x4 = (float4_t *)(x + r0);
+    for (int i = threadIdx.x; i < (H >> 2); i += blockDim.x) {
+      const float4_t xv = x4[i];
+      float4_t d = {0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < S; s0 += C) {
+        float4_t pv[C];
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+          if (s0 + j < S) pv[j] = ((const float4_t *)(part + (size_t)(s0 + j) * MN + r0))[i];
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+          if (s0 + j < S) d += pv[j];
+      }
+      x4[i] = xv + d;
+    }
+  } else {
+    for (int h = threadIdx.x; h < H; h += blockDim.x) {
+      float d = 0.f;
+      for (int s = 0; s < S; ++s) d += part[(size_t)s * MN + r0 + h];
+      x[r0 + h] = x[r0 + h] + d;
+    }
+  }
+  __syncthreads();  // the block's x stores are seen by every wave's norm
+  const float inv = sf_row_inv_rms(x + r0, nullptr, H, eps);
+  for (int h = threadIdx.x; h < H; h += blockDim.x)
+    store_as(out, odt, r0 + h, sf_opaque(x[r0 + h] * inv * load_as(w, wdt, h)));
+}
+
 // ---------------------------------------------------------------------------
 // One wave per (row, head) of the fused q|k|v projection output
 // qkv [rows][(H + 2 KVH) * D]: sf_rope_append_head (rotate-half RoPE with the
@@ -609,6 +649,19 @@ extern "C" int sf_rmsnorm(float *x, const float *delta, const void *w, int w_dty
   k_rmsnorm<<<rows, kThreads, 0, (hipStream_t)stream>>>(x, delta, w, w_dtype, out, out_dtype, H,
                                                          eps);
   return sf_check_launch("sf_rmsnorm");
+}
+
+extern "C" int sf_rmsnorm_partials(float *x, const float *part, int n_parts, const void *w,
+                                   int w_dtype, void *out, int out_dtype, int rows, int H, float eps,
+                                   void *stream) {
+  SF_REQUIRE(rows > 0 && H > 0 && n_parts > 0, SF_EINVAL,
+             "invalid rmsnorm shape rows=%d H=%d n_parts=%d", rows, H, n_parts);
+  SF_REQUIRE(x && part && w && out, SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(w_dtype >= SF_F32 && w_dtype <= SF_BF16 && out_dtype >= SF_F32 && out_dtype <= SF_BF16,
+             SF_EINVAL, "bad rmsnorm dtype");
+  k_rmsnorm_parts<<<rows, kThreads, 0, (hipStream_t)stream>>>(x, part, n_parts, (size_t)rows * H, w,
+                                                              w_dtype, out, out_dtype, H, eps);
+  return sf_check_launch("sf_rmsnorm_partials");
 }
 
 extern "C" int sf_rope_kv_append(const float *qkv, const float *cos_t, const float *sin_t,

@@ -942,14 +942,17 @@ extern "C" size_t sf_q4_gemm_workspace_bytes(int M, int N, int K, int group_size
   return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
-extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
-                          float *y_f32, const void *bias, int bias_dtype, int M, int N, int K,
-                          int group_size, int has_zeros, void *workspace, size_t workspace_bytes,
-                          void *stream) {
+// The GEMM launch; `partials` leaves a split shape's K-split partials in the
+// workspace (no reduce launch, no output) for a consumer that sums them in
+// split order itself.
+static int q4_gemm_impl(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
+                        float *y_f32, const void *bias, int bias_dtype, int M, int N, int K,
+                        int group_size, int has_zeros, void *workspace, size_t workspace_bytes,
+                        void *stream, bool partials) {
   SF_REQUIRE(M > 0 && N > 0 && K > 0 && group_size > 0, SF_EINVAL,
              "invalid shape M=%d N=%d K=%d group_size=%d", M, N, K, group_size);
   SF_REQUIRE(K % group_size == 0, SF_EINVAL, "in_features must be divisible by group_size");
-  SF_REQUIRE(blob && x && (y || y_f32), SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(blob && x && (partials || y || y_f32), SF_EINVAL, "null pointer argument");
   SF_REQUIRE(x_dtype == SF_F16 || x_dtype == SF_BF16 || x_dtype == SF_F32, SF_EINVAL,
              "bad activation dtype %d", x_dtype);
   SF_REQUIRE(y_dtype == SF_F16 || y_dtype == SF_BF16 || y_dtype == SF_F32, SF_EINVAL,
@@ -1048,11 +1051,35 @@ extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y,
 #undef SF_GEMM_X
 #undef SF_GEMM_LAUNCH
   }
-  int rc = sf_check_launch("sf_q4_gemm");
-  if (rc || ksplit == 1) return rc;
+  int rc = sf_check_launch(partials ? "sf_q4_gemm_partials" : "sf_q4_gemm");
+  if (rc || ksplit == 1 || partials) return rc;
   const size_t n8 = ((size_t)M * N + 7) / 8;
   unsigned rg = (unsigned)((n8 + 255) / 256);
   if (rg > 65535u * 16u) rg = 65535u * 16u;
   k_splitk_reduce<<<rg, 256, 0, s>>>(part, y, y_dtype, y_f32, bias, bias_dtype, M, N, ksplit, vec);
   return sf_check_launch("sf_q4_gemm(reduce)");
+}
+
+extern "C" int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtype,
+                          float *y_f32, const void *bias, int bias_dtype, int M, int N, int K,
+                          int group_size, int has_zeros, void *workspace, size_t workspace_bytes,
+                          void *stream) {
+  return q4_gemm_impl(blob, x, x_dtype, y, y_dtype, y_f32, bias, bias_dtype, M, N, K, group_size,
+                      has_zeros, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int sf_q4_gemm_splits(int M, int N, int K, int group_size) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size || group_size % 32) return 0;
+  return choose_ksplit(M, N, K);
+}
+
+extern "C" int sf_q4_gemm_partials(const void *blob, const void *x, int x_dtype, int M, int N,
+                                   int K, int group_size, int has_zeros, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+  const int s = sf_q4_gemm_splits(M, N, K, group_size);
+  SF_REQUIRE(s > 1, SF_EINVAL,
+             "sf_q4_gemm_partials: M=%d N=%d K=%d group_size=%d runs unsplit (use sf_q4_gemm)", M,
+             N, K, group_size);
+  return q4_gemm_impl(blob, x, x_dtype, nullptr, SF_F32, nullptr, nullptr, SF_F32, M, N, K,
+                      group_size, has_zeros, workspace, workspace_bytes, stream, true);
 }

@@ -289,6 +289,40 @@ class LlamaModel:
                                       int(w.has_zeros), None if ws is None else ws.data_ptr(),
                                       0 if ws is None else ws.numel(), self._st()), "sf_q4_gemm")
 
+    def _gemm_delta(self, w: Q4Weight, X: torch.Tensor, Dl: torch.Tensor) -> int:
+        """The projection's output as the residual's delta: where the GEMM
+        splits K, its partials stay in the GEMM workspace for the next
+        RMSNorm to sum (returns their count; no reduce launch), else it is
+        written to Dl (returns 0). Either way the norm gets the same bits."""
+        M = X.shape[0]
+        if not self._gemv_ok(M, w):
+            S = int(self.lib.sf_q4_gemm_splits(M, w.out_features, w.in_features, w.group_size))
+            if S > 1:
+                need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features,
+                                                           w.group_size)
+                if self._gemm_ws is None or self._gemm_ws.numel() < need:
+                    raise SFError(f"GEMM workspace: {need} bytes for {M} rows exceeds the "
+                                  f"preallocated {0 if self._gemm_ws is None else self._gemm_ws.numel()} "
+                                  "(max_prefill)")
+                self._chk(self.lib.sf_q4_gemm_partials(
+                    w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], M, w.out_features, w.in_features,
+                    w.group_size, int(w.has_zeros), self._gemm_ws.data_ptr(), self._gemm_ws.numel(),
+                    self._st()), "sf_q4_gemm_partials")
+                return S
+        self._gemm(w, X, Dl, None)
+        return 0
+
+    def _rmsnorm_delta(self, x, delta, parts: int, w, out, rows):
+        """RMSNorm after adding the residual delta: `parts` K-split partials in
+        the GEMM workspace (from _gemm_delta), else the `delta` rows (or none)."""
+        if not parts:
+            self._rmsnorm(x, delta, w, out, rows)
+            return
+        self._chk(self.lib.sf_rmsnorm_partials(
+            x.data_ptr(), self._gemm_ws.data_ptr(), parts, w.data_ptr(), _lib.SF_F32, out.data_ptr(),
+            _DT[out.dtype], rows, self.H, float(self.config.rms_norm_eps), self._st()),
+            "sf_rmsnorm_partials")
+
     def _gemv_fused(self, w: Q4Weight, src: torch.Tensor, op: int, norm_w, y32: torch.Tensor,
                     bias: torch.Tensor | None):
         self._chk(self.lib.sf_q4_gemv_fused(
@@ -508,11 +542,12 @@ class LlamaModel:
         # without the residual inside the projections, each norm adds the
         # previous projection's output (Dl) to the residual rows itself
         delta = lambda l: None if res or l < 0 else Dl
+        parts = 0  # the previous projection's K-split partials still to add (see _gemm_delta)
         for l, L in enumerate(self.layers):
             if fq:
                 self._gemv_fused_rows(L.qkv, Hb, RMS, L.w_in, QKV, L.qkv_bias, T)
             else:
-                self._rmsnorm(Hb, delta(l - 1), L.w_in, Xn, T)
+                self._rmsnorm_delta(Hb, delta(l - 1), parts, L.w_in, Xn, T)
                 self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
             self._rope_append(l, QKV, Q, T, pos_dev, 0 if dev_pos else self.pos)
             args = (Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
@@ -526,25 +561,27 @@ class LlamaModel:
             else:
                 self._chk(lib.sf_attn_prefill_i8kv(*args, T, self.Hq, self.KVH, self.pos, self.max_seq,
                                                    self.D, self.scale, st), "sf_attn_prefill_i8kv")
+            parts = 0
             if res:
                 self._gemm(L.o, A, Hb, Hb)  # residual add as the bias (per row)
             else:
-                self._gemm(L.o, A, Dl, None)
+                parts = self._gemm_delta(L.o, A, Dl)
             if fg:
                 self._gemv_fused_rows(L.gate_up, Hb, RMS, L.w_post, GU, None, T)
             else:
-                self._rmsnorm(Hb, delta(l), L.w_post, Xn, T)
+                self._rmsnorm_delta(Hb, delta(l), parts, L.w_post, Xn, T)
                 self._gemm(L.gate_up, Xn, GU, None)
             if fd:
                 self._gemv_fused_rows(L.down, GU, SILU, None, Hb, Hb, T)
                 continue
             self._chk(lib.sf_silu_mul(GU.data_ptr(), ACT.data_ptr(), _DT[ACT.dtype], T, self.I, st),
                       "sf_silu_mul")
+            parts = 0
             if res:
                 self._gemm(L.down, ACT, Hb, Hb)
             else:
-                self._gemm(L.down, ACT, Dl, None)
-        self._rmsnorm(Hb, delta(len(self.layers) - 1), self.norm_w, Xn, T)
+                parts = self._gemm_delta(L.down, ACT, Dl)
+        self._rmsnorm_delta(Hb, delta(len(self.layers) - 1), parts, self.norm_w, Xn, T)
 
     # ---------------------------------------------------------------- decode
     def decode_step(self, logits: bool = False) -> None:

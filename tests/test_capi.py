@@ -107,6 +107,33 @@ def test_gemm_workspace_and_validation():
     assert rc == -1 and "in_features must be divisible by group_size" in _lib.last_error()
 
 
+
+def test_gemm_partials_splits_and_validation():
+    """sf_q4_gemm_splits agrees with the workspace sizing (two or more splits
+    exactly where sf_q4_gemm needs a workspace of splits x M x N floats);
+    sf_q4_gemm_partials refuses an unsplit shape and sf_rmsnorm_partials bad
+    arguments, before any launch."""
+    lib = _lib.load()
+    for M, N, K, g in ((512, 4864, 896, 64), (512, 896, 4864, 64), (512, 1152, 896, 64),
+                       (512, 896, 896, 64), (16, 4096, 4096, 128), (9, 896, 4864, 32)):
+        s = lib.sf_q4_gemm_splits(M, N, K, g)
+        wsb = lib.sf_q4_gemm_workspace_bytes(M, N, K, g)
+        assert s >= 1 and (s > 1) == (wsb > 0)
+        assert s == 1 or wsb == s * M * N * 4
+    assert lib.sf_q4_gemm_splits(512, 896, 4864, 64) == 8   # 28 tiles: split 8 ways
+    assert lib.sf_q4_gemm_splits(512, 896, 4848, 48) == 0   # group 48: the VALU kernel
+    assert lib.sf_q4_gemm_splits(512, 896, 4864, 0) == 0
+    blob, x = 256 * 1024, 4096  # fake addresses: validation fails before any use
+    rc = lib.sf_q4_gemm_partials(blob, x, 2, 512, 4864, 896, 64, 0, None, 0, None)
+    assert rc == -1 and "runs unsplit" in _lib.last_error()
+    rc = lib.sf_q4_gemm_partials(blob, x, 2, 512, 896, 4864, 64, 0, None, 0, None)
+    assert rc == -1 and "workspace too small" in _lib.last_error()
+    rc = lib.sf_rmsnorm_partials(None, None, 2, None, 0, None, 0, 4, 896, 1e-6, None)
+    assert rc == -1 and "null pointer argument" in _lib.last_error()
+    rc = lib.sf_rmsnorm_partials(x, x, 0, x, 0, x, 0, 4, 896, 1e-6, None)
+    assert rc == -1 and "n_parts=0" in _lib.last_error()
+
+
 def test_attention_validation_and_sizes():
     lib = _lib.load()
     acc = 14 * 256 * 64 * 4  # split acc, then (m, l) at the next 256-byte boundary

@@ -138,3 +138,52 @@ def test_gemm_unit_vector_rows_pin_mapping(dev, xdtype):
     Y = w.matmul(torch.as_tensor(X).to(dev).to(xdtype), out_dtype=torch.float32).cpu().numpy()
     exp = (q[:, kk].astype(np.float64) * s[:, kk // g]).T
     np.testing.assert_array_equal(Y, exp.astype(np.float32))
+
+
+@pytest.mark.parametrize("N,K,has_zeros", [(896, 4864, True), (896, 896, False), (896, 896, True)])
+def test_gemm_partials_fold_into_rmsnorm(dev, N, K, has_zeros):
+    """The prompt path's o / down projections: sf_q4_gemm_partials leaves the
+    K-split partials and sf_rmsnorm_partials adds them to the residual rows and
+    normalizes. Residual rows and normed outputs equal, bit for bit, the reduce
+    into a delta buffer followed by sf_rmsnorm (the path they replace)."""
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(N + K)
+    W = laplace_outliers(rng, (N, K))
+    if has_zeros:
+        pk, s, z = P.pack_weights_asym(W, 64)
+    else:
+        (pk, s), z = P.pack_weights_sym(W, 64), None
+    w = Q4Weight(pk, s, z, 64, device=dev)
+    M = 512
+    S = lib.sf_q4_gemm_splits(M, N, K, 64)
+    assert S > 1
+    X = torch.as_tensor(rng.normal(0, 1, (M, K)).astype(np.float32)).to(dev).half().contiguous()
+    h0 = torch.as_tensor(rng.normal(0, 1, (M, N)).astype(np.float32)).to(dev)
+    nw = torch.as_tensor(rng.uniform(0.5, 1.5, N).astype(np.float32)).to(dev)
+    wsb = lib.sf_q4_gemm_workspace_bytes(M, N, K, 64)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    F32, F16 = _lib.SF_F32, _lib.SF_F16
+    # the reduce path
+    Dl = torch.empty((M, N), dtype=torch.float32, device=dev)
+    x1, o1 = h0.clone(), torch.empty((M, N), dtype=torch.float16, device=dev)
+    _lib.check(lib.sf_q4_gemm(w.blob.data_ptr(), X.data_ptr(), F16, None, F32, Dl.data_ptr(), None, F32,
+                              M, N, K, 64, int(has_zeros), ws.data_ptr(), wsb, st), "sf_q4_gemm")
+    _lib.check(lib.sf_rmsnorm(x1.data_ptr(), Dl.data_ptr(), nw.data_ptr(), F32, o1.data_ptr(), F16, M, N,
+                              1e-6, st), "sf_rmsnorm")
+    # the partials path (the workspace first filled with something else)
+    ws.fill_(0x7F)
+    x2, o2 = h0.clone(), torch.empty((M, N), dtype=torch.float16, device=dev)
+    _lib.check(lib.sf_q4_gemm_partials(w.blob.data_ptr(), X.data_ptr(), F16, M, N, K, 64, int(has_zeros),
+                                       ws.data_ptr(), wsb, st), "sf_q4_gemm_partials")
+    _lib.check(lib.sf_rmsnorm_partials(x2.data_ptr(), ws.data_ptr(), S, nw.data_ptr(), F32, o2.data_ptr(),
+                                       F16, M, N, 1e-6, st), "sf_rmsnorm_partials")
+    torch.cuda.synchronize()
+    assert torch.equal(x1.view(torch.int32), x2.view(torch.int32))
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    # and the delta itself against the oracle's GEMM
+    ref = linear.gemm(pk, s16(s), X.float().cpu().numpy().astype(np.float64), 64,
+                      zeros=z)
+    linear.assert_close((x2 - h0).double().cpu().numpy(), ref, 1e-3, f"partials delta [{N},{K}]")
