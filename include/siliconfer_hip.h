@@ -325,6 +325,18 @@ int sf_rope_kv_append(const float *qkv, const float *cos_t, const float *sin_t, 
                       void *v_scales, int scale_dtype, int rows, int H, int KVH, int D, int T_cap,
                       const int *pos_dev, int pos_host, void *stream);
 
+/* sf_rope_kv_append with the q|k|v rows given as the n_parts K-split partials
+ * of sf_q4_gemm_partials (partial s at part[s * rows * W + r * W + c],
+ * W = (H + 2 KVH) * D) plus the projection's bias [W] (or NULL): each value
+ * summed in split order from 0, then the bias added. The same bits as
+ * sf_q4_gemm(..., bias) into a qkv buffer followed by sf_rope_kv_append, with
+ * one launch less (no counterpart in the reference; layers.py:99-112). */
+int sf_rope_kv_append_partials(const float *part, int n_parts, const void *bias, int bias_dtype,
+                               const float *cos_t, const float *sin_t, int max_pos, void *q_out,
+                               int q_dtype, int8_t *k_codes, void *k_scales, int8_t *v_codes,
+                               void *v_scales, int scale_dtype, int rows, int H, int KVH, int D,
+                               int T_cap, const int *pos_dev, int pos_host, void *stream);
+
 /* SwiGLU activation (layers.py:143-144): out[r][i] = silu(gu[r][i]) *
  * gu[r][I + i] for the fused gate|up projection rows gu [rows][2 I]. */
 int sf_silu_mul(const float *gu, void *out, int out_dtype, int rows, int I, void *stream);

@@ -82,6 +82,9 @@ _SIGS = {
                                    _c_p]),
     "sf_rope_kv_append": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p,
                                  _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_i, _c_p]),
+    "sf_rope_kv_append_partials": (_c_i, [_c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i,
+                                          _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                          _c_i, _c_p, _c_i, _c_p]),
     "sf_silu_mul": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_i, _c_p]),
     "sf_lm_head_workspace_bytes": (_c_sz, [_c_i]),
     "sf_lm_head_argmax": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p,

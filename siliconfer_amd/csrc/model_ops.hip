@@ -122,6 +122,39 @@ k_rope_kv_append(const float *__restrict__ qkv, SfRopeAppend a, const int *__res
   sf_rope_append_head(a, qkv + (size_t)row * width + (size_t)head * a.D, head, pos, row);
 }
 
+// k_rope_kv_append with the q|k|v rows as S K-split partials (MN apart) of the
+// projection plus its bias: each value summed in split order from 0, then the
+// bias added (the GEMM reduce's arithmetic, so the head sees the values the
+// reduce would have stored), staged in LDS for the head.
+__global__ void __launch_bounds__(64)
+k_rope_kv_append_parts(const float *__restrict__ part, int S, size_t MN,
+                       const void *__restrict__ bias, int bdt, SfRopeAppend a,
+                       const int *__restrict__ pos_dev, int pos_host) {
+  __shared__ float xs[256];
+  const int row = blockIdx.x, head = blockIdx.y;
+  const int pos = (pos_dev ? *pos_dev : pos_host) + row;
+  if (pos < 0 || pos >= a.T_cap || pos >= a.max_pos) return;  // the host keeps positions in range
+  const int width = (a.H + 2 * a.KVH) * a.D;
+  const size_t base = (size_t)row * width + (size_t)head * a.D;
+  constexpr int C = 8;  // partials whose loads go out together
+  for (int d = threadIdx.x; d < a.D; d += 64) {
+    float v = 0.f;
+    for (int s0 = 0; s0 < S; s0 += C) {
+      float pv[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (s0 + j < S) pv[j] = part[(size_t)(s0 + j) * MN + base + d];
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (s0 + j < S) v += pv[j];
+    }
+    if (bias) v += load_as(bias, bdt, (size_t)head * a.D + d);
+    xs[d] = v;
+  }
+  __syncthreads();
+  sf_rope_append_head(a, xs, head, pos, row);
+}
+
 // ---------------------------------------------------------------------------
 // out[r][i] = silu(gu[r][i]) * gu[r][I + i], silu(g) = g / (1 + exp(-g)).
 __global__ void __launch_bounds__(kThreads)
@@ -687,6 +720,38 @@ extern "C" int sf_rope_kv_append(const float *qkv, const float *cos_t, const flo
                        v_scales, scale_dtype, H, KVH, D, T_cap};
   k_rope_kv_append<<<grid, 64, 0, (hipStream_t)stream>>>(qkv, a, pos_dev, pos_host);
   return sf_check_launch("sf_rope_kv_append");
+}
+
+extern "C" int sf_rope_kv_append_partials(const float *part, int n_parts, const void *bias,
+                                          int bias_dtype, const float *cos_t, const float *sin_t,
+                                          int max_pos, void *q_out, int q_dtype, int8_t *k_codes,
+                                          void *k_scales, int8_t *v_codes, void *v_scales,
+                                          int scale_dtype, int rows, int H, int KVH, int D,
+                                          int T_cap, const int *pos_dev, int pos_host,
+                                          void *stream) {
+  SF_REQUIRE(n_parts > 0, SF_EINVAL, "invalid n_parts=%d", n_parts);
+  SF_REQUIRE(!bias || (bias_dtype >= SF_F32 && bias_dtype <= SF_BF16), SF_EINVAL,
+             "bad bias dtype %d", bias_dtype);
+  SF_REQUIRE(rows > 0 && H > 0 && KVH > 0 && D > 0 && T_cap > 0 && max_pos > 0, SF_EINVAL,
+             "invalid rope/append shape rows=%d H=%d KVH=%d D=%d T_cap=%d", rows, H, KVH, D,
+             T_cap);
+  SF_REQUIRE(D % 2 == 0 && D <= 256, SF_EUNSUPPORTED, "head_dim=%d: need an even D <= 256", D);
+  SF_REQUIRE(part && cos_t && sin_t && q_out && k_codes && k_scales && v_codes && v_scales,
+             SF_EINVAL, "null pointer argument");
+  SF_REQUIRE(q_dtype >= SF_F32 && q_dtype <= SF_BF16, SF_EINVAL, "bad q dtype %d", q_dtype);
+  SF_REQUIRE(scale_dtype == SF_F16 || scale_dtype == SF_F32, SF_EINVAL, "bad scale dtype %d",
+             scale_dtype);
+  if (!pos_dev)
+    SF_REQUIRE(pos_host >= 0 && pos_host + rows <= T_cap && pos_host + rows <= max_pos, SF_EINVAL,
+               "positions %d..%d exceed the cache capacity %d or the RoPE table %d", pos_host,
+               pos_host + rows - 1, T_cap, max_pos);
+  dim3 grid(rows, H + 2 * KVH);
+  const SfRopeAppend a{cos_t, sin_t, max_pos, q_out, q_dtype, k_codes, k_scales, v_codes,
+                       v_scales, scale_dtype, H, KVH, D, T_cap};
+  const size_t MN = (size_t)rows * (H + 2 * KVH) * D;
+  k_rope_kv_append_parts<<<grid, 64, 0, (hipStream_t)stream>>>(part, n_parts, MN, bias,
+                                                               bias_dtype, a, pos_dev, pos_host);
+  return sf_check_launch("sf_rope_kv_append_partials");
 }
 
 extern "C" int sf_silu_mul(const float *gu, void *out, int out_dtype, int rows, int I,

@@ -289,28 +289,34 @@ class LlamaModel:
                                       int(w.has_zeros), None if ws is None else ws.data_ptr(),
                                       0 if ws is None else ws.numel(), self._st()), "sf_q4_gemm")
 
-    def _gemm_delta(self, w: Q4Weight, X: torch.Tensor, Dl: torch.Tensor) -> int:
-        """The projection's output as the residual's delta: where the GEMM
-        splits K, its partials stay in the GEMM workspace for the next
-        RMSNorm to sum (returns their count; no reduce launch), else it is
-        written to Dl (returns 0). Either way the norm gets the same bits."""
+    def _gemm_parts(self, w: Q4Weight, X: torch.Tensor) -> int:
+        """Where the GEMM splits K for these rows, run it leaving its partials
+        in the GEMM workspace (no reduce launch) and return their count; else
+        launch nothing and return 0."""
         M = X.shape[0]
-        if not self._gemv_ok(M, w):
-            S = int(self.lib.sf_q4_gemm_splits(M, w.out_features, w.in_features, w.group_size))
-            if S > 1:
-                need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features,
-                                                           w.group_size)
-                if self._gemm_ws is None or self._gemm_ws.numel() < need:
-                    raise SFError(f"GEMM workspace: {need} bytes for {M} rows exceeds the "
-                                  f"preallocated {0 if self._gemm_ws is None else self._gemm_ws.numel()} "
-                                  "(max_prefill)")
-                self._chk(self.lib.sf_q4_gemm_partials(
-                    w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], M, w.out_features, w.in_features,
-                    w.group_size, int(w.has_zeros), self._gemm_ws.data_ptr(), self._gemm_ws.numel(),
-                    self._st()), "sf_q4_gemm_partials")
-                return S
-        self._gemm(w, X, Dl, None)
-        return 0
+        if self._gemv_ok(M, w):
+            return 0
+        S = int(self.lib.sf_q4_gemm_splits(M, w.out_features, w.in_features, w.group_size))
+        if S <= 1:
+            return 0
+        need = self.lib.sf_q4_gemm_workspace_bytes(M, w.out_features, w.in_features, w.group_size)
+        if self._gemm_ws is None or self._gemm_ws.numel() < need:
+            raise SFError(f"GEMM workspace: {need} bytes for {M} rows exceeds the preallocated "
+                          f"{0 if self._gemm_ws is None else self._gemm_ws.numel()} (max_prefill)")
+        self._chk(self.lib.sf_q4_gemm_partials(
+            w.blob.data_ptr(), X.data_ptr(), _DT[X.dtype], M, w.out_features, w.in_features,
+            w.group_size, int(w.has_zeros), self._gemm_ws.data_ptr(), self._gemm_ws.numel(),
+            self._st()), "sf_q4_gemm_partials")
+        return S
+
+    def _gemm_delta(self, w: Q4Weight, X: torch.Tensor, Dl: torch.Tensor) -> int:
+        """The projection's output as the residual's delta: its K-split
+        partials left for the next RMSNorm to sum (returns their count), else
+        written to Dl (returns 0). Either way the norm gets the same bits."""
+        S = self._gemm_parts(w, X)
+        if not S:
+            self._gemm(w, X, Dl, None)
+        return S
 
     def _rmsnorm_delta(self, x, delta, parts: int, w, out, rows):
         """RMSNorm after adding the residual delta: `parts` K-split partials in
@@ -342,6 +348,14 @@ class LlamaModel:
             _DT[q_out.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
             self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, rows, self.Hq,
             self.KVH, self.D, self.max_seq, pos_dev, pos_host, self._st()), "sf_rope_kv_append")
+
+    def _rope_append_parts(self, l, parts, bias, q_out, rows, pos_dev, pos_host):
+        self._chk(self.lib.sf_rope_kv_append_partials(
+            self._gemm_ws.data_ptr(), parts, None if bias is None else bias.data_ptr(), _lib.SF_F32,
+            self.cos.data_ptr(), self.sin.data_ptr(), self.max_seq, q_out.data_ptr(),
+            _DT[q_out.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
+            self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, rows, self.Hq,
+            self.KVH, self.D, self.max_seq, pos_dev, pos_host, self._st()), "sf_rope_kv_append_partials")
 
     def _lm_head_norm(self, h_row, token, pos_inc, logits=True):
         self._chk(self.lib.sf_lm_head_argmax_rmsnorm(
@@ -544,12 +558,18 @@ class LlamaModel:
         delta = lambda l: None if res or l < 0 else Dl
         parts = 0  # the previous projection's K-split partials still to add (see _gemm_delta)
         for l, L in enumerate(self.layers):
+            qparts = 0  # q|k|v left as K-split partials for RoPE + append to sum
             if fq:
                 self._gemv_fused_rows(L.qkv, Hb, RMS, L.w_in, QKV, L.qkv_bias, T)
             else:
                 self._rmsnorm_delta(Hb, delta(l - 1), parts, L.w_in, Xn, T)
-                self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
-            self._rope_append(l, QKV, Q, T, pos_dev, 0 if dev_pos else self.pos)
+                qparts = self._gemm_parts(L.qkv, Xn)
+                if not qparts:
+                    self._gemm(L.qkv, Xn, QKV, L.qkv_bias)
+            if qparts:
+                self._rope_append_parts(l, qparts, L.qkv_bias, Q, T, pos_dev, 0 if dev_pos else self.pos)
+            else:
+                self._rope_append(l, QKV, Q, T, pos_dev, 0 if dev_pos else self.pos)
             args = (Q.data_ptr(), _DT[Q.dtype], self.k_codes[l].data_ptr(), self.k_scales[l].data_ptr(),
                     self.v_codes[l].data_ptr(), self.v_scales[l].data_ptr(), _lib.SF_F16, A.data_ptr(),
                     _DT[A.dtype])

@@ -132,6 +132,10 @@ def test_gemm_partials_splits_and_validation():
     assert rc == -1 and "null pointer argument" in _lib.last_error()
     rc = lib.sf_rmsnorm_partials(x, x, 0, x, 0, x, 0, 4, 896, 1e-6, None)
     assert rc == -1 and "n_parts=0" in _lib.last_error()
+    rope = lambda n, bdt: lib.sf_rope_kv_append_partials(x, n, x, bdt, x, x, 64, x, 1, x, x, x, x, 1,
+                                                          4, 14, 2, 64, 64, None, 0, None)
+    assert rope(0, _lib.SF_F32) == -1 and "n_parts=0" in _lib.last_error()
+    assert rope(2, 7) == -1 and "bad bias dtype 7" in _lib.last_error()
 
 
 def test_attention_validation_and_sizes():

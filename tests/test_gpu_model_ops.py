@@ -251,3 +251,56 @@ def test_prefill_attention_shapes(dev, monkeypatch, kernel, D, H, KVH, T0, Tq, T
     V = vc[0].astype(np.float32) * vs[0].astype(np.float32)[..., None]
     ref = OM.attend(q.float().cpu().numpy(), K, V, T0, D ** -0.5)
     assert_close(out.cpu().numpy(), ref, 2e-3, f"prefill {kernel} D={D} H={H}/{KVH} T0={T0} Tq={Tq}")
+
+
+def test_rope_append_from_gemm_partials(dev):
+    """The prompt path's qkv projection: sf_q4_gemm_partials + sf_rope_kv_append_partials
+    (partials summed in split order, bias added) store the same q rows, KV codes and
+    scales, bit for bit, as sf_q4_gemm(..., bias) into a qkv buffer + sf_rope_kv_append."""
+    from oracle import primitives as P
+    from siliconfer_amd.kernels import Q4Weight
+
+    lib = _lib.load()
+    rng = np.random.default_rng(11)
+    M, H, KVH, D, K, T_cap = 512, 14, 2, 64, 896, 600
+    N = (H + 2 * KVH) * D
+    pk, s = P.pack_weights_sym(rng.normal(0, 0.02, (N, K)).astype(np.float32), 64)
+    w = Q4Weight(pk, s, None, 64, device=dev)
+    S = lib.sf_q4_gemm_splits(M, N, K, 64)
+    assert S > 1
+    X = torch.as_tensor(rng.normal(0, 1, (M, K)).astype(np.float32)).to(dev).half().contiguous()
+    bias = torch.as_tensor(rng.normal(0, 0.1, N).astype(np.float32)).to(dev)
+    pos = np.arange(T_cap)[:, None] * (1e6 ** (-np.arange(0, D, 2) / D))[None, :]
+    cos = torch.as_tensor(np.cos(pos).astype(np.float32)).to(dev)
+    sin = torch.as_tensor(np.sin(pos).astype(np.float32)).to(dev)
+    wsb = lib.sf_q4_gemm_workspace_bytes(M, N, K, 64)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def cache():
+        return (torch.zeros((M, H, D), dtype=torch.float16, device=dev),
+                torch.zeros((KVH, T_cap, D), dtype=torch.int8, device=dev),
+                torch.zeros((KVH, T_cap), dtype=torch.float16, device=dev),
+                torch.zeros((KVH, T_cap, D), dtype=torch.int8, device=dev),
+                torch.zeros((KVH, T_cap), dtype=torch.float16, device=dev))
+
+    def ptrs(c):
+        q, kc, ks, vc, vs = c
+        return (cos.data_ptr(), sin.data_ptr(), T_cap, q.data_ptr(), F16, kc.data_ptr(), ks.data_ptr(),
+                vc.data_ptr(), vs.data_ptr(), F16, M, H, KVH, D, T_cap, None, 40)
+
+    qkv = torch.empty((M, N), dtype=torch.float32, device=dev)
+    c1, c2 = cache(), cache()
+    _lib.check(lib.sf_q4_gemm(w.blob.data_ptr(), X.data_ptr(), F16, None, F32, qkv.data_ptr(),
+                              bias.data_ptr(), F32, M, N, K, 64, 0, ws.data_ptr(), wsb, st), "sf_q4_gemm")
+    _lib.check(lib.sf_rope_kv_append(qkv.data_ptr(), *ptrs(c1), st), "sf_rope_kv_append")
+    ws.fill_(0x7F)
+    _lib.check(lib.sf_q4_gemm_partials(w.blob.data_ptr(), X.data_ptr(), F16, M, N, K, 64, 0,
+                                       ws.data_ptr(), wsb, st), "sf_q4_gemm_partials")
+    _lib.check(lib.sf_rope_kv_append_partials(ws.data_ptr(), S, bias.data_ptr(), F32, *ptrs(c2), st),
+               "sf_rope_kv_append_partials")
+    torch.cuda.synchronize()
+    for a, b in zip(c1, c2):
+        assert torch.equal(a.view(torch.uint8) if a.dtype == torch.int8 else a.view(torch.int16),
+                           b.view(torch.uint8) if b.dtype == torch.int8 else b.view(torch.int16))
+    assert bool((c2[2][:, 40:40 + M] > 0).all())  # every appended row has its scale
