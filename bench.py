@@ -509,7 +509,10 @@ def e2e_speculative(dev, reps: int = 20):
     draft; the verify / decode cost ratio is the figure that carries over."""
     import torch
 
-    from siliconfer_amd.engine import speculative_generate
+    from siliconfer_amd.engine import SamplingParams, speculative_generate
+
+    def G(n):  # greedy, n tokens
+        return SamplingParams(temperature=0.0, max_tokens=n)
 
     cfg, t, ids = e2e_model(dev, torch.float16)
     t.capture()
@@ -547,8 +550,8 @@ def e2e_speculative(dev, reps: int = 20):
     out = {"decode_step_ms": round(decode_ms, 4), "verify_ms": verify,
            "verify8_over_decode": round(verify[8] / decode_ms, 3)}
     for K in (3, 7):
-        speculative_generate(draft, t, ids, max_tokens=32, K=K)
-        r = speculative_generate(draft, t, ids, max_tokens=E2E_TOKENS, K=K)
+        speculative_generate(draft, t, ids, G(32), K=K)
+        r = speculative_generate(draft, t, ids, G(E2E_TOKENS), K=K)
         out[f"K{K}"] = {"tok_s": round(r.effective_tok_s, 1),
                         "acceptance": round(r.acceptance_rate, 3), "rounds": r.total_rounds}
     return out

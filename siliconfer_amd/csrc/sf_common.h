@@ -92,7 +92,6 @@ __device__ __forceinline__ float sf_bf16_to_f32(uint16_t b) {
   return sf_bitcast<float>((uint32_t)b << 16);
 }
 
-// round-to-nearest-even float -> bf16 bits (NaN kept quiet)
 // fp32 -> bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32; NaN stays NaN)
 __device__ __forceinline__ uint16_t sf_f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);

@@ -20,8 +20,12 @@ How it runs on MI355X:
     temperature, top-k, top-p nucleus, generate.py:24-67) and written back as
     the step's token.
 
-`quantize_kv_cache` is accepted for call compatibility: this decoder's cache is
-always the int8 one (the reference's `quantize_kv_cache=True` path).
+KV cache: this decoder keeps the int8 cache (the reference's
+`quantize_kv_cache=True` path, kv_cache.py:49-126) and has no full-precision one.
+`quantize_kv_cache=True` and the default (None) run it; `False` raises, rather
+than give int8-cache numerics to a caller who asked for the reference's fp16
+cache. A call that leaves the flag out gets the int8 cache where the reference's
+default is the fp16 one (generate.py:124, 135).
 """
 
 from __future__ import annotations
@@ -38,7 +42,16 @@ from ..model.llama import GenerationResult, LlamaModel
 
 CHUNK = 16  # decode steps replayed between host reads when tokens are needed early
 
-__all__ = ["SamplingParams", "sample_token", "GenerationResult", "warmup", "generate"]
+__all__ = ["SamplingParams", "sample_token", "GenerationResult", "warmup", "generate",
+           "check_kv_cache_flag"]
+
+
+def check_kv_cache_flag(quantize_kv_cache) -> None:
+    """The decoders here keep an int8 KV cache only: refuse an explicit
+    request for the reference's full-precision cache."""
+    if quantize_kv_cache is not None and not quantize_kv_cache:
+        raise SFError("quantize_kv_cache=False: this decoder keeps an int8 KV cache only "
+                      "(pass True or leave it unset)")
 
 
 @dataclass
@@ -80,11 +93,11 @@ def sample_token(logits: torch.Tensor, params: SamplingParams,
     return int(torch.multinomial(probs, 1, generator=generator).item())
 
 
-def warmup(model: LlamaModel, quantize_kv_cache: bool = False) -> None:
+def warmup(model: LlamaModel, quantize_kv_cache: bool | None = None) -> None:
     """Record the decode-step graph and run a two-token prompt and one decode
     step, so the first timed `generate` pays no one-time set-up (the
     reference warms MLX's lazy compilation the same way, generate.py:89-114)."""
-    del quantize_kv_cache
+    check_kv_cache_flag(quantize_kv_cache)
     if model.graph is None:
         model.capture()
     model.reset()
@@ -110,13 +123,13 @@ def _prompt_array(prompt_ids) -> np.ndarray:
 def generate(model: LlamaModel, prompt_ids, params: SamplingParams | None = None,
              eos_token_id: int | None = None, stream: bool = False,
              on_token: Callable[[int], None] | None = None,
-             quantize_kv_cache: bool = False,
+             quantize_kv_cache: bool | None = None,
              generator: torch.Generator | None = None) -> GenerationResult:
     """Prefill the prompt, then decode up to `params.max_tokens - 1` more
     tokens, stopping after `eos_token_id`. `on_token` gets every token as it
     is produced (else `stream` prints it); `decode_tok_s` counts the tokens
     after the first over the time after prefill, as the reference does."""
-    del quantize_kv_cache
+    check_kv_cache_flag(quantize_kv_cache)
     params = params or SamplingParams()
     ids = _prompt_array(prompt_ids)
     if ids.size + params.max_tokens > model.max_seq + 1:
@@ -139,10 +152,13 @@ def generate(model: LlamaModel, prompt_ids, params: SamplingParams | None = None
     t0 = time.perf_counter()
     first = model.prefill(ids, want_logits=not greedy)
     if not greedy:
+        torch.cuda.synchronize(model.device)
+    t1 = time.perf_counter()  # the prefill clock stops before the first draw (generate.py:139-141)
+    if not greedy:
         first = sample_token(model.logits, params, out, generator)
         model.token.fill_(first)
-    t1 = time.perf_counter()
     emit(first)
+    t_dec = time.perf_counter()  # decode clock after the first token (generate.py:152)
     budget = params.max_tokens - 1
     done = eos_token_id is not None and first == eos_token_id
     while budget > 0 and not done:
@@ -170,6 +186,6 @@ def generate(model: LlamaModel, prompt_ids, params: SamplingParams | None = None
             budget -= 1
     torch.cuda.synchronize(model.device)
     t2 = time.perf_counter()
-    if stream and on_token is None:
+    if stream:
         print()
-    return GenerationResult(out, t1 - t0, t2 - t1, int(ids.size), len(out) - 1)
+    return GenerationResult(out, t1 - t0, t2 - t_dec, int(ids.size), len(out) - 1)

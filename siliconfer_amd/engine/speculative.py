@@ -1,28 +1,49 @@
-"""Greedy speculative decoding over two int4 decoders on one GPU — the
-reference's siliconfer.engine.speculative (/root/reference/siliconfer/engine/
-speculative.py:151-365) at temperature 0.
+"""Speculative decoding over two int4 decoders on one GPU — the reference's
+siliconfer.engine.speculative (/root/reference/siliconfer/engine/
+speculative.py:151-365), same signature:
+
+    speculative_generate(draft, target, prompt_ids, params=None, K=4,
+                         eos_token_id=None, on_token=None, seed=None,
+                         dynamic_K=False, K_min=1, K_max=8,
+                         quantize_kv_cache=None)
 
 Each round (speculative.py:259-352):
-  1. the draft proposes K tokens from the last committed token: K decode
-     steps, replayed from the draft's HIP graph without a host round trip;
+  1. the draft proposes K tokens from the last committed token;
   2. the target verifies [cur, d_0 .. d_{K-1}] in one forward
      (`LlamaModel.verify`: K + 1 <= 8 rows run every projection as one batch
-     GEMV, so the verify streams the target's weights once; it replays the
-     target's verify graph for K + 1 rows, recorded on first use);
-  3. d_q is accepted while it equals the target's greedy token after row q
-     (`_tok_prob` at temperature 0 gives 1 or 0, :44-51); the first mismatch
-     is replaced by the target's token, and a fully accepted round adds the
-     target's bonus token after row K (:286-303);
+     GEMV, so the verify streams the target's weights once);
+  3. d_q is accepted with probability min(1, p_target(d_q) / p_draft(d_q))
+     (:285-297); the first rejection is replaced by a draw from
+     max(0, p_target - p_draft) / Z (`_sample_adjusted`, :62-84), and a fully
+     accepted round adds a draw from the target's row K (:298-303);
   4. both KV caches are trimmed to the committed length N + j + 1
      (`LlamaModel.set_position`, the cache `trim` of :29-41); when every draft
      token was accepted the draft runs d_{K-1} to catch up (:336-343);
   5. with `dynamic_K`, K grows by one after a fully accepted round and shrinks
      by one after a rejection, within [K_min, K_max] (:311-315).
 
-The committed tokens are the target's own greedy choices at every position,
-so the output is the target's greedy generation; the draft only decides how
-many tokens one verify commits. Sampling at temperature > 0 is not part of
-this build (the decoders pick greedily on the device)."""
+At temperature 0 (`params.temperature <= 0`) every probability is 1 or 0
+(`_tok_prob`, :44-51), so d_q is accepted exactly when it equals the target's
+greedy token: the draft's K steps replay its decode graph (each step feeds its
+token to the next on the device) and the target's verify replays one graph per
+K + 1, with the greedy pick of each row made on the device. At temperature > 0
+the draft steps and the verify run eagerly and keep their fp32 logits; the
+draws use torch on the device from a generator seeded with `seed` (the
+reference seeds MLX's generator and draws its acceptance uniforms from
+Python's `random`; both are replaced by the one seeded torch generator). As in
+the reference, sampling here uses the temperature only (no top-k / top-p /
+repetition penalty, :53-59).
+
+Differences a caller can see:
+  * K + 1 must fit the verify's 8 rows: K > 7 raises; with `dynamic_K`, K
+    grows to at most min(K_max, 7) (K never enters the acceptance rule, so the
+    output distribution is the same);
+  * the decoders keep int8 KV caches: `quantize_kv_cache=False` raises
+    (`True` and the default are the int8 cache);
+  * `draft is target` runs the draft on `target.sibling()` (shared weights, a
+    cache of its own), since a `LlamaModel` owns its cache where the
+    reference's models take one as an argument.
+"""
 
 from __future__ import annotations
 
@@ -34,6 +55,9 @@ import numpy as np
 import torch
 
 from .._lib import SFError
+from .generate import SamplingParams, check_kv_cache_flag
+
+VERIFY_MAX_ROWS = 8  # rows of one verify forward (LlamaModel.VERIFY_ROWS)
 
 
 @dataclass
@@ -74,40 +98,90 @@ def accept_greedy(draft_tokens: list[int], target_tokens: list[int]) -> tuple[in
     return j, target_tokens[j]
 
 
-def speculative_generate(draft, target, prompt_ids, max_tokens: int = 128, K: int = 4,
-                         eos_token_id: int | None = None,
-                         on_token: Callable[[int], None] | None = None, dynamic_K: bool = False,
-                         K_min: int = 1, K_max: int = 7, temperature: float = 0.0,
-                         ) -> SpeculativeResult:
-    """Greedy speculative generation with `draft` proposing and `target`
-    verifying (both LlamaModel on the same device, same vocabulary).
+def _probs(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    return torch.softmax(logits.float() / temperature, dim=-1)
 
-    The draft must have a captured decode graph (`draft.capture()`); the
-    target runs only prefill and verify. Both caches need room for the prompt,
-    max_tokens and one round's K + 1 rows. `max_tokens` counts every generated
-    token, the first (from the prefill) included, as SamplingParams.max_tokens
-    does in the reference (speculative.py:259)."""
-    if temperature > 0.0:
-        raise SFError("speculative decoding here is greedy (temperature 0)")
-    if draft.V != target.V:
-        raise SFError("draft and target vocabularies differ")
-    if draft.graph is None:
-        raise SFError("capture() the draft's decode step first")
+
+def _sample_logits(logits: torch.Tensor, temperature: float, gen: torch.Generator) -> int:
+    """A draw from softmax(logits / T) (speculative.py:53-59)."""
+    return int(torch.multinomial(_probs(logits, temperature), 1, generator=gen).item())
+
+
+def _sample_adjusted(t_logits: torch.Tensor, d_logits: torch.Tensor, temperature: float,
+                     gen: torch.Generator) -> int:
+    """A draw from max(0, p_target - p_draft) / Z, or from p_target when Z
+    vanishes (speculative.py:62-84)."""
+    adj = torch.clamp(_probs(t_logits, temperature) - _probs(d_logits, temperature), min=0.0)
+    total = float(adj.sum().item())
+    if total < 1e-10:
+        return _sample_logits(t_logits, temperature, gen)
+    return int(torch.multinomial(adj / total, 1, generator=gen).item())
+
+
+def accept_sampled(draft_tokens: list[int], draft_logits: list[torch.Tensor],
+                   target_logits: torch.Tensor, temperature: float,
+                   gen: torch.Generator) -> tuple[int, int]:
+    """(j, replacement) of one sampled round (speculative.py:285-303): d_q is
+    accepted with probability min(1, p_t(d_q) / (p_d(d_q) + 1e-12)); the
+    first rejection is replaced from the adjusted distribution, a fully
+    accepted round draws the bonus from the target's row K."""
+    K = len(draft_tokens)
+    if target_logits.shape[0] != K + 1:
+        raise SFError(f"verify returned {target_logits.shape[0]} rows for {K} draft tokens")
+    for q in range(K):
+        tok = draft_tokens[q]
+        p_t = float(_probs(target_logits[q], temperature)[tok].item())
+        p_d = float(_probs(draft_logits[q], temperature)[tok].item())
+        u = float(torch.rand((), generator=gen, device=gen.device).item())
+        if u < min(1.0, p_t / (p_d + 1e-12)):
+            continue
+        return q, _sample_adjusted(target_logits[q], draft_logits[q], temperature, gen)
+    return K, _sample_logits(target_logits[K], temperature, gen)
+
+
+def speculative_generate(draft, target, prompt_ids, params: SamplingParams | None = None,
+                         K: int = 4, eos_token_id: int | None = None,
+                         on_token: Callable[[int], None] | None = None, seed: int | None = None,
+                         dynamic_K: bool = False, K_min: int = 1, K_max: int = 8,
+                         quantize_kv_cache: bool | None = None) -> SpeculativeResult:
+    """Speculative generation with `draft` proposing and `target` verifying
+    (both LlamaModel on the same device, same vocabulary). Argument meaning as
+    in the reference (speculative.py:151-233); `params.max_tokens` counts
+    every generated token, the first (from the prefill) included. Both caches
+    need room for the prompt, max_tokens and one round's K + 1 rows."""
+    params = params if params is not None else SamplingParams()
+    check_kv_cache_flag(quantize_kv_cache)
+    if K + 1 > VERIFY_MAX_ROWS:
+        raise SFError(f"K={K}: the verify forward takes at most {VERIFY_MAX_ROWS} rows "
+                      f"(K <= {VERIFY_MAX_ROWS - 1})")
     if not 1 <= K_min <= K <= K_max:
         raise SFError(f"need 1 <= K_min <= K <= K_max (got {K_min}, {K}, {K_max})")
-    ids = np.asarray(prompt_ids, dtype=np.int64).reshape(-1)
+    k_cap = min(K_max, VERIFY_MAX_ROWS - 1)
+    if draft is target:
+        draft = target.sibling()
+    if draft.V != target.V:
+        raise SFError("draft and target vocabularies differ")
+    temp = float(params.temperature)
+    greedy = temp <= 0.0
+    if greedy and draft.graph is None:
+        draft.capture()
+    max_tokens = int(params.max_tokens)
+    ids = np.asarray(prompt_ids.detach().cpu() if isinstance(prompt_ids, torch.Tensor) else prompt_ids,
+                     dtype=np.int64).reshape(-1)
     T = int(ids.size)
-    need = T + max_tokens + K_max + 1
+    need = T + max_tokens + k_cap + 1
     for m, name in ((draft, "draft"), (target, "target")):
         if need > m.max_seq:
             raise SFError(f"the {name} cache holds {m.max_seq} positions; prompt + max_tokens + "
                           f"K_max + 1 = {need}")
     dev = torch.device(target.device)
-    # one verify graph per batch K+1 the rounds can use (recorded once)
-    sizes = {k + 1 for k in range(K_min, K_max + 1) if k + 1 <= 8}
-    missing = sorted(sizes - target.verify_graph_sizes)
-    if missing:
-        target.capture_verify(missing)
+    if greedy:  # one verify graph per batch K+1 the rounds can use (recorded once)
+        sizes = {k + 1 for k in range(K_min, k_cap + 1)}
+        missing = sorted(sizes - target.verify_graph_sizes)
+        if missing:
+            target.capture_verify(missing)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(int(seed) if seed is not None else int(torch.randint(0, 2 ** 62, ()).item()))
 
     def sync():
         if dev.type == "cuda":
@@ -117,10 +191,12 @@ def speculative_generate(draft, target, prompt_ids, max_tokens: int = 128, K: in
     target.reset()
     sync()
     t0 = time.perf_counter()
-    cur = target.prefill(ids, want_logits=False)
+    cur = target.prefill(ids, want_logits=not greedy)
     draft.prefill(ids, want_logits=False)
     sync()
     t_prefill = time.perf_counter()
+    if not greedy:
+        cur = _sample_logits(target.logits, temp, gen)
 
     generated = [cur]
     if on_token is not None:
@@ -131,18 +207,32 @@ def speculative_generate(draft, target, prompt_ids, max_tokens: int = 128, K: in
     t_dec = time.perf_counter()
     while len(generated) < max_tokens:
         round_K = cur_K
-        # draft: round_K greedy steps from cur at positions N .. N+K-1 (each
-        # step writes its token to hist[position] and feeds it to the next)
         draft.token.fill_(cur)
-        draft.replay(round_K)
-        d = draft.hist[N:N + round_K].tolist()
+        if greedy:
+            # round_K greedy steps from cur at positions N .. N+K-1 (each step
+            # writes its token to hist[position] and feeds it to the next)
+            draft.replay(round_K)
+            d = draft.hist[N:N + round_K].tolist()
+            # target: one forward over [cur, d_0 .. d_{K-1}] at positions N .. N+K
+            j, replacement = accept_greedy(d, target.verify([cur] + d))
+        else:
+            d, d_logits = [], []
+            for _ in range(round_K):
+                p = draft.pos
+                draft.decode_step(logits=True)
+                draft.pos += 1
+                row = draft.logits.clone()
+                tok = _sample_logits(row, temp, gen)
+                draft.token.fill_(tok)
+                draft.hist[p] = tok
+                d.append(tok)
+                d_logits.append(row)
+            target.verify([cur] + d, want_logits=True)
+            j, replacement = accept_sampled(d, d_logits, target.vlogits[:round_K + 1], temp, gen)
         drafted += round_K
-        # target: one forward over [cur, d_0 .. d_{K-1}] at positions N .. N+K
-        t = target.verify([cur] + d)
-        j, replacement = accept_greedy(d, t)
         accepted += j
         if dynamic_K:
-            cur_K = min(round_K + 1, K_max) if j == round_K else max(round_K - 1, K_min)
+            cur_K = min(round_K + 1, k_cap) if j == round_K else max(round_K - 1, K_min)
         new_batch = (d[:j] + [replacement])[:max_tokens - len(generated)]
         for tok in new_batch:
             generated.append(tok)
@@ -153,7 +243,12 @@ def speculative_generate(draft, target, prompt_ids, max_tokens: int = 128, K: in
         new_N = N + j + 1
         target.set_position(new_N)
         if j == round_K:  # the draft's last step left d_{K-1} as its input token
-            draft.replay(1)
+            if greedy:
+                draft.replay(1)
+            else:
+                draft.token.fill_(d[-1])
+                draft.decode_step()
+                draft.pos += 1
         else:
             draft.set_position(new_N)
         N = new_N

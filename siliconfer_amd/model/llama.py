@@ -181,6 +181,15 @@ class LlamaModel:
                                                                  w.group_size))
         self._gemm_ws = torch.empty(ws, dtype=torch.uint8, device=dev) if ws else None
 
+    def sibling(self) -> "LlamaModel":
+        """A decoder over the same device weights with a KV cache, buffers and
+        graphs of its own: the second cache that the reference's models get by
+        taking the cache as an argument (speculative decoding with draft ==
+        target, engine/speculative.py:224-225)."""
+        return LlamaModel(self.config, self.layers, self.embed, self.norm_w, self.group_size,
+                          self.max_seq, act_dtype=self.act_dtype, max_prefill=self.max_prefill,
+                          fuse=self.fuse, lm_head=None if self.head is self.embed else self.head)
+
     # ------------------------------------------------------------------ init
     @classmethod
     def random_init(cls, config: ModelConfig, seed: int = 4, group_size: int = 64,
@@ -587,10 +596,12 @@ class LlamaModel:
             else:
                 parts = self._gemm_delta(L.o, A, Dl)
             if fg:
+                assert parts == 0, "the folded RMSNorm reads no K-split partials"
                 self._gemv_fused_rows(L.gate_up, Hb, RMS, L.w_post, GU, None, T)
             else:
                 self._rmsnorm_delta(Hb, delta(l), parts, L.w_post, Xn, T)
                 self._gemm(L.gate_up, Xn, GU, None)
+            parts = 0  # consumed: the o projection's partials are in Hb now
             if fd:
                 self._gemv_fused_rows(L.down, GU, SILU, None, Hb, Hb, T)
                 continue

@@ -8,8 +8,10 @@ maps [..., in_features] -> [..., out_features] and adds `bias`.
 Where the reference evaluates the MLX graph, copies x to the host and runs the
 CPU GEMM on every call (q4_linear.py:51-63), this layer keeps the weights in
 HBM as a repacked blob and runs entirely on the device stream: rows <= 8 go to
-the decode GEMV, more rows to the MFMA prefill GEMM. The output has x's dtype
-(fp16 / bf16 / fp32); accumulation is fp32 either way.
+the decode GEMV, more rows to the MFMA prefill GEMM. The output is fp32 like
+the reference's (it casts x to fp32 and its GEMM returns fp32, q4_linear.py:55-63);
+fp16 / bf16 x are read as they are, which equals the reference's upcast since
+every fp16 / bf16 value is exact in fp32. The bias is added in fp32.
 """
 
 from __future__ import annotations
@@ -50,10 +52,9 @@ class Q4Linear(torch.nn.Module):
         x2 = x.reshape(-1, self.in_features)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        b = self.bias
-        if b is not None and b.dtype != x2.dtype and x2.dtype != torch.float32:
-            b = b.to(x2.dtype)
-        y = self.weight.matmul(x2, out_dtype=x2.dtype, bias=b)
+        if x2.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            x2 = x2.float()
+        y = self.weight.matmul(x2, out_dtype=torch.float32, bias=self.bias)
         return y.reshape(*orig[:-1], self.out_features)
 
     __call__ = torch.nn.Module.__call__

@@ -86,7 +86,7 @@ def hqq_quantize_weight(W: np.ndarray, group_size: int = 128, p: float = 0.7,
     """Fake-quantized fp32 weights [N, K] from the HQQ search. A matrix with
     in_features < group_size is one group per row, plain asymmetric RTN
     (the reference's fallback, hqq.py:116-120)."""
-    W = np.asarray(W, np.float32)
+    W = np.asarray(W)  # the search runs in float64 from the caller's values (hqq.py:122)
     N, K = W.shape
     if K < group_size:
         if bits != 4:

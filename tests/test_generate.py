@@ -65,3 +65,23 @@ def test_prompt_shapes():
         _prompt_array([[1, 2], [3, 4]])
     with pytest.raises(SFError):
         _prompt_array([])
+
+
+def test_reference_signatures():
+    """generate / speculative_generate keep the reference's parameter order
+    (engine/generate.py:117-125, engine/speculative.py:151-164); the KV-cache
+    flag defaults to the int8 cache and refuses an explicit False."""
+    import inspect
+
+    from siliconfer_amd.engine import check_kv_cache_flag, generate, speculative_generate
+
+    assert list(inspect.signature(generate).parameters)[:7] == [
+        "model", "prompt_ids", "params", "eos_token_id", "stream", "on_token", "quantize_kv_cache"]
+    sp = inspect.signature(speculative_generate).parameters
+    assert list(sp) == ["draft", "target", "prompt_ids", "params", "K", "eos_token_id", "on_token",
+                        "seed", "dynamic_K", "K_min", "K_max", "quantize_kv_cache"]
+    assert sp["K"].default == 4 and sp["K_max"].default == 8 and sp["K_min"].default == 1
+    check_kv_cache_flag(None)
+    check_kv_cache_flag(True)
+    with pytest.raises(RuntimeError, match="int8 KV cache only"):
+        check_kv_cache_flag(False)

@@ -200,6 +200,31 @@ def test_bias_and_output_dtypes(dev):
         linear.assert_close(y, ref, TOL + rounding, f"bias {od}")
 
 
+def test_bf16_output_rounding_bits(dev):
+    """The bf16 output conversion (sf_f32_to_bf16: gfx950's v_cvt_pk_bf16_f32)
+    pinned bit for bit against torch's round-to-nearest-even cast: zero
+    weights make each output exactly its fp32 bias, which holds ties (both
+    ways to even), values just off a tie, bf16 subnormals and their ties,
+    the largest finite values (one rounds to infinity), infinities and NaN."""
+    N = 64
+    pk = np.zeros((N, 64), np.uint8)
+    s = np.ones((N, 2), np.float32)
+    u = lambda bits: np.uint32(bits).view(np.float32)
+    vals = [1.0, u(0x3F808000), u(0x3F818000), u(0x3F808001), u(0x3F817FFF), -u(0x3F808000),
+            u(0x00008000), u(0x00018000), u(0x00000001), u(0x00010000), u(0x0000FFFF),
+            -u(0x00008000), u(0x7F7FFFFF), u(0x7F7F7FFF), u(0x7F7F8000), np.inf, -np.inf,
+            np.nan, u(0x3EAAAAAB), 65504.0, 1e-40, -3.0e38]
+    b = np.zeros(N, np.float32)
+    b[:len(vals)] = np.asarray(vals, np.float32)
+    x = np.random.default_rng(9).normal(0, 1, (1, 128)).astype(np.float16)
+    _, y, _ = run_gemv(dev, pk, s, None, x, 64, bias=b, out_dtype=torch.bfloat16)
+    want = torch.from_numpy(b).to(torch.bfloat16).view(torch.int16).numpy()
+    got = torch.from_numpy(y[0].astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy()
+    nan = np.isnan(b)
+    assert np.array_equal(got[~nan], want[~nan]), np.nonzero(got != want)
+    assert np.all(np.isnan(y[0][nan]))
+
+
 def test_repeated_launches_bitwise_identical(dev):
     """The reduction order is fixed: repeated calls give identical bits
     (the reference's race check, tests/test_metal_attention.py:87-103)."""

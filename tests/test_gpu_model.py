@@ -187,9 +187,12 @@ def test_config5_full_workload_against_oracle(dev):
     Qwen2.5-0.5B geometry, seed 4, int4 sym g=64, fp16 activations, the 512-id
     prompt, then 255 decode steps replayed from the HIP graph. The oracle runs
     teacher-forced on the GPU's own tokens (prompt + generated, one causal
-    block, pinned equal to token-by-token decoding): every greedy token must be
-    the oracle's pick wherever its top-2 margin clears the tolerance, and the
-    logits of the prefill and of 9 spread decode steps must meet 1e-2
+    block, pinned equal to token-by-token decoding). Every one of the 256
+    steps is checked: its logits meet 1e-2 against the oracle's, its token is
+    the argmax of its own logits (lowest index on ties), and the token is the
+    oracle's argmax, or, where the oracle's top-2 margin is within twice that
+    step's measured logit error (a near-tie that rounding may resolve either
+    way), a logit within that distance of the oracle's maximum
     (reference harness: /root/reference/siliconfer/engine/generate.py:117-180)."""
     cfg = ModelConfig.qwen25_05b()
     m = LlamaModel.random_init(cfg, seed=4, group_size=64, device=dev, max_seq=512 + 256 + 256,
@@ -198,24 +201,34 @@ def test_config5_full_workload_against_oracle(dev):
     m.capture(logits=True)
     m.reset()
     first = m.prefill(ids)
-    glog = {-1: m.logits.cpu().numpy().copy()}
-    spread = {0, 1, 2, 37, 85, 128, 170, 213, 254}
+    glog = [m.logits.cpu().numpy().copy()]
     for i in range(255):
         m.replay(1)
-        if i in spread:
-            torch.cuda.synchronize()
-            glog[i] = m.logits.cpu().numpy().copy()
+        torch.cuda.synchronize()
+        glog.append(m.logits.cpu().numpy().copy())
     toks = [first] + m.hist[512:512 + 255].cpu().tolist()
     W = m.export_weights()
     cos, sin = rope_tables(cfg, m.max_seq)
     ref = OM.forward(W, cfg, np.concatenate([ids, np.asarray(toks[:-1])]), OM.KVCache(24), cos, sin,
                      last_rows=256)
     tol = 1e-2
-    checked = 0
+    exact = ties = 0
+    worst = 0.0
     for j in range(256):  # ref[j]: the logits after position 511 + j, which picked toks[j]
-        if margin_ok(ref[j], tol):
-            checked += 1
-            assert toks[j] == OM.greedy(ref[j]), f"config 5 token {j}"
-    assert checked >= 64, f"only {checked} of 256 steps had a clear top-2 margin"
-    for i, got in glog.items():
-        assert_close(got, ref[i + 1], tol, f"config 5 logits after decode step {i}")
+        got, r = glog[j], ref[j]
+        assert_close(got, r, tol, f"config 5 logits of step {j}")
+        worst = max(worst, float(np.abs(got - r).max() / np.abs(r).max()))
+        assert toks[j] == int(np.argmax(got)), f"config 5 step {j}: token is not its logits' argmax"
+        err = float(np.abs(got - r).max())
+        best = OM.greedy(r)
+        if toks[j] == best:
+            exact += 1
+        else:
+            top2 = np.sort(r)[-2:]
+            assert top2[1] - top2[0] <= 2 * err and r[toks[j]] >= r[best] - 2 * err, (
+                f"config 5 step {j}: token {toks[j]}, oracle {best}, margin {top2[1] - top2[0]:.3g} "
+                f"against twice the step's logit error {2 * err:.3g}")
+            ties += 1
+    print(f"config 5: 256 steps checked, {exact} tokens equal to the oracle's argmax, {ties} "
+          f"near-ties resolved the other way; worst logit error {worst:.2e} of max |logit|")
+    assert exact + ties == 256

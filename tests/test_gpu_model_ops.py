@@ -222,6 +222,7 @@ def test_causal_prefill_attention(dev, T0, Tq):
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
 @pytest.mark.parametrize("D,H,KVH,T0,Tq,T_cap", [
     (64, 14, 2, 0, 16, 16),       # the smallest flash chunk, cache exactly full
+    (64, 14, 2, 0, 24, 64),       # first workgroups see one key tile: three of their waves have none
     (64, 14, 2, 5, 333, 341),     # T_cap % 4 != 0 (per-token scale loads)
     (128, 32, 2, 0, 100, 128),    # 16 query heads per kv head, head_dim 128
     (128, 8, 8, 40, 70, 112),     # MHA

@@ -20,7 +20,7 @@ import torch
 from oracle import model as OM
 from oracle.linear import assert_close
 from siliconfer_amd import _lib
-from siliconfer_amd.engine import speculative_generate
+from siliconfer_amd.engine import SamplingParams, speculative_generate
 from siliconfer_amd.model.config import ModelConfig, rope_tables
 from siliconfer_amd.model.llama import LlamaModel
 
@@ -37,6 +37,10 @@ TINY_DRAFT = ModelConfig(hidden_size=128, intermediate_size=256, num_hidden_laye
 
 def st():
     return torch.cuda.current_stream().cuda_stream
+
+
+def G(n):  # greedy parameters for n tokens
+    return SamplingParams(temperature=0.0, max_tokens=n)
 
 
 def near_tie(logits: np.ndarray, a: int, b: int, tol: float) -> bool:
@@ -274,8 +278,8 @@ def test_speculative_equals_target_greedy(dev, act, K, dynamic):
     for name, draft in drafts.items():
         draft.capture()
         seen = []
-        r = speculative_generate(draft, target, prompt, max_tokens=40, K=K, dynamic_K=dynamic,
-                                 K_max=7, on_token=seen.append)
+        r = speculative_generate(draft, target, prompt, G(40), K=K, dynamic_K=dynamic,
+                                 on_token=seen.append)
         assert len(r.token_ids) == 40 and seen == r.token_ids and r.num_decode_tokens == 39
         assert r.total_accepted <= r.total_draft_tokens
         assert target.pos == draft.pos == len(prompt) + r.total_rounds + r.total_accepted
@@ -291,13 +295,46 @@ def test_speculative_eos_stops(dev):
     target.capture()
     draft.capture()
     prompt = np.random.default_rng(57).integers(0, SMALL.vocab_size, 10)
-    full = speculative_generate(draft, target, prompt, max_tokens=30, K=4).token_ids
+    full = speculative_generate(draft, target, prompt, G(30), K=4).token_ids
     # eos: the token whose first appearance after the prefill token comes last
     # (the prefill token itself is not checked for eos, speculative.py:243-351)
     first_at = {}
     for i in range(1, len(full)):
         first_at.setdefault(full[i], i)
     eos, stop = max(first_at.items(), key=lambda kv: kv[1])
-    r = speculative_generate(draft, target, prompt, max_tokens=30, K=4, eos_token_id=eos)
+    r = speculative_generate(draft, target, prompt, G(30), K=4, eos_token_id=eos)
     # stops after the round that committed eos: at most K tokens after it
     assert r.token_ids == full[:len(r.token_ids)] and stop < len(r.token_ids) <= stop + 1 + 4
+
+
+def test_speculative_draft_is_target(dev):
+    """draft=target, the reference tests' setting (test_speculative.py:125-137):
+    the draft runs on a sibling decoder (same weights, own cache), so every
+    greedy proposal is accepted and the output is the target's greedy one."""
+    target = LlamaModel.random_init(SMALL, seed=58, group_size=64, device=dev, max_seq=128)
+    target.capture()
+    prompt = np.random.default_rng(59).integers(0, SMALL.vocab_size, 9)
+    r = speculative_generate(target, target, prompt, G(24), 3, None, None, 0)  # reference order
+    assert len(r.token_ids) == 24 and r.acceptance_rate == 1.0
+    assert r.token_ids == target.generate(prompt, max_tokens=24).token_ids
+    with pytest.raises(RuntimeError, match="at most 8 rows"):
+        speculative_generate(target, target, prompt, G(8), K=8)
+    with pytest.raises(RuntimeError, match="int8 KV cache only"):
+        speculative_generate(target, target, prompt, G(8), quantize_kv_cache=False)
+
+
+def test_speculative_sampled(dev):
+    """Temperature > 0 (speculative.py:285-303): valid ids, max_tokens honoured,
+    the same seed gives the same tokens, and a draft identical to the target
+    has every proposal accepted (p_target / p_draft = 1 up to rounding)."""
+    target = LlamaModel.random_init(SMALL, seed=60, group_size=64, device=dev, max_seq=128)
+    draft = LlamaModel.random_init(TINY_DRAFT, seed=61, group_size=64, device=dev, max_seq=128)
+    prompt = np.random.default_rng(62).integers(0, SMALL.vocab_size, 8)
+    p = SamplingParams(temperature=0.8, max_tokens=20)
+    a = speculative_generate(draft, target, prompt, p, K=3, seed=5, dynamic_K=True, K_max=6)
+    b = speculative_generate(draft, target, prompt, p, K=3, seed=5, dynamic_K=True, K_max=6)
+    assert len(a.token_ids) == 20 and all(0 <= t < SMALL.vocab_size for t in a.token_ids)
+    assert a.token_ids == b.token_ids and a.total_rounds == b.total_rounds
+    assert target.pos == draft.pos == len(prompt) + a.total_rounds + a.total_accepted
+    same = speculative_generate(target, target, prompt, p, K=4, seed=7)
+    assert same.acceptance_rate > 0.95 and len(same.token_ids) == 20
