@@ -378,6 +378,38 @@ int sf_lm_head_argmax_rows(const void *w, const void *x, int x_dtype, float *log
                            int B, int32_t *tokens_out, void *workspace, size_t workspace_bytes,
                            void *stream);
 
+/* ---- a chain of dependent decode GEMVs in one persistent launch (no
+ * counterpart in the reference, which runs each Q4Linear of a layer as its own
+ * call, /root/reference/siliconfer/model/layers.py:93-95, 133, 139-144) -------
+ * y = W_{n-1} f(... f(W_1 f(W_0 x0))): phase p multiplies the symmetric int4
+ * blob blobs[p] ([N[p], K[p]], group group[p]: 64 or a multiple of 128; K[p] a
+ * multiple of 128 up to 12288) by its input, at batch 1. Phase 0 reads x0
+ * (fp16 [K[0]]); phase p > 0 reads the first K[p] of phase p-1's fp32 outputs
+ * rounded to fp16 (in_kind[p] = SF_CHAIN_IN_PREV, N[p-1] >= K[p]) or silu(gate) * up of them
+ * (SF_CHAIN_IN_SWIGLU: gate = outputs [0, K[p]), up = [K[p], 2 K[p]),
+ * N[p-1] == 2 K[p]); in_kind[0] = SF_CHAIN_IN_X0. The last phase's fp32 output
+ * goes to y_f32. One workgroup per CU runs every phase; a workgroup issues a
+ * phase's weight loads before it waits for the phase's input, which it reads
+ * from the workspace as tagged words (value + launch tag in one 8-byte atomic
+ * word). The workspace (sf_q4_chain_workspace_bytes(N, nph), 256-byte aligned)
+ * must be zero-filled once before its first call and then kept: it holds the
+ * launch counter the tags come from. Calls that overlap on one workspace race.
+ * Every wait is bounded by spin_cap rounds (~1-2 us each; 1 << 20 for
+ * production use): on expiry the kernel records an error in the workspace and
+ * exits normally with wrong results; sf_q4_chain_error (synchronous) returns
+ * that error (0: none) and the workspace keeps it. drop_phase >= 0 is a test
+ * hook: that phase's outputs are not published, so its consumers' waits
+ * expire (-1 for normal use). */
+#define SF_CHAIN_MAX_PHASES 8
+#define SF_CHAIN_IN_X0 0
+#define SF_CHAIN_IN_PREV 1
+#define SF_CHAIN_IN_SWIGLU 2
+size_t sf_q4_chain_workspace_bytes(const int *N, int nph);
+int sf_q4_chain(const void *const *blobs, const int *N, const int *K, const int *group,
+                const int *in_kind, int nph, const void *x0_f16, float *y_f32, void *workspace,
+                size_t workspace_bytes, int spin_cap, int drop_phase, void *stream);
+int sf_q4_chain_error(const void *workspace, int *err_out, void *stream);
+
 /* ---- measurement floor (no counterpart in the reference: the reference only
  * assumes a peak bandwidth, scripts/benchmark.py:26) ----------------------
  * sf_floor_empty: one empty one-wave launch (the per-launch cost of the queue).

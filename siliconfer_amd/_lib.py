@@ -21,6 +21,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsiliconf
 
 SF_F32, SF_F16, SF_BF16 = 0, 1, 2
 SF_PRE_RMSNORM, SF_PRE_SILU_MUL = 1, 2
+SF_CHAIN_IN_X0, SF_CHAIN_IN_PREV, SF_CHAIN_IN_SWIGLU = 0, 1, 2
+SF_CHAIN_MAX_PHASES = 8
 _DT = {torch.float32: SF_F32, torch.float16: SF_F16, torch.bfloat16: SF_BF16}
 
 _c_i, _c_f, _c_sz, _c_p = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
@@ -94,6 +96,10 @@ _SIGS = {
     "sf_lm_head_rows_workspace_bytes": (_c_sz, [_c_i, _c_i]),
     "sf_lm_head_argmax_rows": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz,
                                       _c_p]),
+    "sf_q4_chain_workspace_bytes": (_c_sz, [_c_p, _c_i]),
+    "sf_q4_chain": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_i, _c_i,
+                           _c_p]),
+    "sf_q4_chain_error": (_c_i, [_c_p, _c_p, _c_p]),
     "sf_floor_empty": (_c_i, [_c_p]),
     "sf_floor_read": (_c_i, [_c_p, _c_sz, _c_p, _c_p]),
 }
