@@ -71,6 +71,7 @@ def ref_lib():
         lib.ref_q4_gemv_sym_scalar.argtypes = [_u8p, _f32p, _f32p, _f32p, _i, _i, _i]
         lib.ref_q4_gemv_sym.argtypes = [_u8p, _f32p, _f32p, _f32p, _i, _i, _i]
         lib.ref_q4_gemm_sym.argtypes = [_u8p, _f32p, _f32p, _f32p, _i, _i, _i, _i]
+        lib.ref_q4_gemv_sym_rows.argtypes = [_u8p, _f32p, _f32p, _f32p, _i, _i, _i, _i]
         _ref = lib
     return _ref
 
@@ -94,6 +95,19 @@ def gemv_sym(packed, scales, x, group_size, nthreads=1, impl="port"):
                                          _ptr(y, _f32p), N, 2 * Kh, group_size)
     else:
         raise ValueError(impl)
+    return y
+
+
+def gemv_sym_ref_rows(packed, scales, x, group_size, parts=1):
+    """The reference's q4_gemv_sym (q4_gemv.cpp:240-247, scalar on x86) over
+    `parts` row slices on an OpenMP team of `parts` threads (ref_glue.cpp).
+    Each row's sum is the reference's own; only the rows are dealt out.
+    packed/scales must already be contiguous u8 / fp32."""
+    N, Kh = packed.shape
+    x = _c(x, np.float32).reshape(-1)
+    y = np.empty(N, dtype=np.float32)
+    ref_lib().ref_q4_gemv_sym_rows(_ptr(packed, _u8p), _ptr(scales, _f32p), _ptr(x, _f32p),
+                                   _ptr(y, _f32p), N, 2 * Kh, group_size, parts)
     return y
 
 

@@ -115,10 +115,18 @@ def residual(x: np.ndarray, delta: np.ndarray) -> np.ndarray:
     return x + delta
 
 
+def dense(L: dict, name: str, x: np.ndarray) -> np.ndarray:
+    """Projection `name` of layer dict L over rows x: x @ W.T with the
+    dequantized fp32 weight (Q4Linear's math, q4_linear.py:49-68)."""
+    return x @ L[name].T
+
+
 def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: np.ndarray,
-            last_rows: int | None = None) -> np.ndarray:
+            last_rows: int | None = None, linear=dense) -> np.ndarray:
     """Run tokens `ids` (appending to `cache`) and return the logits of every
-    row [T, V], or of the last `last_rows` rows only."""
+    row [T, V], or of the last `last_rows` rows only. `linear(L, name, x)`
+    computes each projection (default: `dense`; the CPU baseline passes the
+    reference's own int4 kernel over the packed weights)."""
     ids = np.asarray(ids, dtype=np.int64).reshape(-1)
     T = ids.size
     H, Hq, KVH, D = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -128,7 +136,7 @@ def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: n
     x = weights["embed"][ids].astype(np.float32)
     for l, L in enumerate(weights["layers"]):
         xn = rmsnorm(x, L["w_in"], eps)
-        qkv = xn @ L["qkv"].T
+        qkv = linear(L, "qkv", xn)
         if L["qkv_bias"] is not None:
             qkv = qkv + L["qkv_bias"]
         q = qkv[:, :Hq * D].reshape(T, Hq, D)
@@ -138,10 +146,10 @@ def forward(weights: dict, cfg, ids, cache: KVCache, cos_t: np.ndarray, sin_t: n
         k = rope(k, pos, cos_t, sin_t)
         K, V = cache.append(l, k, v.astype(np.float32))
         a = attend(q, K, V, pos0, D ** -0.5).reshape(T, Hq * D)
-        x = residual(x, a @ L["o"].T)
+        x = residual(x, linear(L, "o", a))
         xn = rmsnorm(x, L["w_post"], eps)
-        act = swiglu(xn @ L["gate_up"].T, cfg.intermediate_size)
-        x = residual(x, act @ L["down"].T)
+        act = swiglu(linear(L, "gate_up", xn), cfg.intermediate_size)
+        x = residual(x, linear(L, "down", act))
     if last_rows is not None:
         x = x[-last_rows:]
     xn = rmsnorm(x, weights["norm"], eps)

@@ -229,9 +229,12 @@ class LlamaModel:
         norm_w = torch.ones(H, dtype=torch.float32, device=dev)
         return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill, fuse)
 
-    def export_weights(self) -> dict:
+    def export_weights(self, packed: bool = False) -> dict:
         """Host copies for a reference restatement: dequantized fp32 weights
-        (fp16 scales as stored), biases, norms, the embedding as fp32."""
+        (fp16 scales as stored), biases, norms, the embedding as fp32. With
+        `packed`, each projection also as `name + "_q4"`: (codes u8 [N, K/2] in
+        the reference's nibble order, scales fp32 [N, G], group size), the
+        operands of the reference's q4_gemv_sym (symmetric weights only)."""
         out = {"embed": self.embed.float().cpu().numpy(), "norm": self.norm_w.cpu().numpy(),
                "layers": []}
         if self.head is not self.embed:
@@ -253,6 +256,10 @@ class LlamaModel:
                 else:          # unsigned codes minus the group's zero-point
                     q = q.astype(np.float32).reshape(q.shape[0], -1, g) - z.cpu().numpy()[..., None]
                 d[name] = (q * s[..., None]).reshape(pk.shape[0], -1)
+                if packed:
+                    if z is not None:
+                        raise ValueError("packed export takes symmetric weights")
+                    d[name + "_q4"] = (np.ascontiguousarray(pk), np.ascontiguousarray(s, np.float32), g)
             d["qkv_bias"] = None if L.qkv_bias is None else L.qkv_bias.cpu().numpy()
             d["w_in"], d["w_post"] = L.w_in.cpu().numpy(), L.w_post.cpu().numpy()
             out["layers"].append(d)

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import model as OM
+from oracle import cpu, model as OM
+from oracle import primitives as P
 from siliconfer_amd.model.config import ModelConfig, RoPEScalingConfig, rope_freqs, rope_tables
 
 
@@ -102,6 +103,36 @@ def test_causal_block_equals_token_by_token():
     cache = OM.KVCache(2)
     rows = [OM.forward(W, cfg, [t], cache, cos, sin)[0] for t in ids]
     np.testing.assert_allclose(block, np.stack(rows), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.skipif(not cpu.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_forward_through_reference_kernel_equals_dense():
+    """The config-5 CPU baseline's path: every projection by the reference's
+    q4_gemv_sym over the packed codes gives the dense forward over the same
+    dequantized weights (fp32 sums in another order: 1e-4)."""
+    cfg = ModelConfig(hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16, vocab_size=50,
+                      rms_norm_eps=1e-6, rope_theta=10000.0, attention_bias=True)
+    rng = np.random.default_rng(5)
+    W = tiny_weights(cfg, rng)
+    for L in W["layers"]:
+        for name in ("qkv", "o", "gate_up", "down"):
+            pk, s = P.pack_weights_sym(L[name], 32)
+            s32 = np.ascontiguousarray(s, np.float32)
+            L[name + "_q4"] = (np.ascontiguousarray(pk), s32, 32)
+            L[name] = P.dequant_packed(pk, s32, None, 32).astype(np.float32)
+    cos, sin = rope_tables(cfg, 32)
+    ids = [3, 17, 5, 42, 9, 0]
+    def lin(L, name, x):
+        pk, s32, g = L[name + "_q4"]
+        return np.stack([cpu.gemv_sym_ref_rows(pk, s32, r, g, 3) for r in x])
+
+    for f in (OM.dense, lin):
+        cache = OM.KVCache(2)
+        rows = [OM.forward(W, cfg, [t], cache, cos, sin, linear=f)[0] for t in ids]
+        if f is OM.dense:
+            dense = np.stack(rows)
+    np.testing.assert_allclose(np.stack(rows), dense, rtol=1e-4, atol=1e-5)
 
 
 def test_pack_sym_device_matches_numpy_packer():

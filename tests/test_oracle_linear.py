@@ -48,6 +48,21 @@ def test_oracle_matches_live_reference_at_config_widths(N, K, g):
     linear.assert_close(linear.gemv(pk, s, x, g), y_ref, 1e-5, "live reference")
 
 
+@pytest.mark.skipif(not cpu.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("parts", [1, 3, 7])
+def test_reference_row_split_equals_whole_call(parts):
+    """The CPU baseline's all-cores leg deals rows of the reference's own
+    kernel to threads: every row's bits equal the single call's."""
+    rng = np.random.default_rng(parts)
+    W = rng.normal(0, 0.02, (1157, 896)).astype(np.float32)
+    x = rng.normal(0, 1, 896).astype(np.float32)
+    pk, s = P.pack_weights_sym(W, 64)
+    s = np.ascontiguousarray(s, np.float32)
+    whole = cpu.gemv_sym(pk, s, x, 64, impl="reference")
+    split = cpu.gemv_sym_ref_rows(np.ascontiguousarray(pk), s, x, 64, parts)
+    np.testing.assert_array_equal(split, whole)
+
+
 def test_oracle_matches_literal_loop():
     rng = np.random.default_rng(2)
     W = rng.normal(0, 1, (6, 128)).astype(np.float32)
