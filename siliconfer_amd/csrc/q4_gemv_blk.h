@@ -502,19 +502,22 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
           for (int s = 0; s < MS; ++s)
             if (s < a.ms) M = fmaxf(M, mq[s].x);
           const float mref = sf_merge_mref(M);
-          float L = 0.f;
+          const int P = sf_merge_span(a.ms);
+          float w[MS], tl[MS];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = 0.f;
+          for (int s = 0; s < MS; ++s) {
+            w[s] = s < a.ms ? sf_merge_weight(mq[s].x, mref) : 0.f;
+            tl[s] = s < a.ms ? sf_merge_term(mq[s].y, w[s]) : 0.f;
+          }
+          const float L = sf_tree_sum(tl, P);
 #pragma unroll
-          for (int s = 0; s < MS; ++s)
-            if (s < a.ms) {
-              const float w = sf_merge_weight(mq[s].x, mref);
-              L = fmaf(mq[s].y, w, L);
+          for (int e = 0; e < 8; ++e) {
+            float tv[MS];
 #pragma unroll
-              for (int e = 0; e < 8; ++e) f[e] = fmaf(sf_bitcast<float>(aq[s][e / 4][e % 4]), w, f[e]);
-            }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = sf_merge_finish(L, f[e]);
+            for (int s = 0; s < MS; ++s)
+              tv[s] = s < a.ms ? sf_merge_term(sf_bitcast<float>(aq[s][e / 4][e % 4]), w[s]) : 0.f;
+            f[e] = sf_merge_finish(L, sf_tree_sum(tv, P));
+          }
         } else {
           piece_values<XDT, PRE>(xq[q], PRE == PRE_RMSNORM ? inv_s[b] : 1.f, f);
         }

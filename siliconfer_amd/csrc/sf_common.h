@@ -177,6 +177,42 @@ __device__ __forceinline__ float2_t sf_swap32_pair(float v) {
   return float2_t{sf_bitcast<float>((uint32_t)r[0]), sf_bitcast<float>((uint32_t)r[1])};
 }
 
+// A pairwise tree across aligned groups of GS lanes (GS = 1, 2, 4, ..., 64;
+// uniform): every lane of a group gets the group's tree sum, the levels those
+// of sf_wave_sum (once a block of lanes holds one value, the mirrors pair it
+// with the next block; each level adds a value and its partner, so both get
+// the same bits). Branch-free: every level is computed, those at or past GS
+// are dropped by a select. All 64 lanes must be active. sf_group_tree_max:
+// the same groups' max.
+__device__ __forceinline__ float sf_group_tree_max(float v, int GS) {
+  float t = fmaxf(v, sf_dpp<0xB1>(v));
+  v = GS > 1 ? t : v;
+  t = fmaxf(v, sf_dpp<0x4E>(v));
+  v = GS > 2 ? t : v;
+  t = fmaxf(v, sf_dpp<0x141>(v));
+  v = GS > 4 ? t : v;
+  t = fmaxf(v, sf_dpp<0x140>(v));
+  v = GS > 8 ? t : v;
+  float2_t p = sf_swap16_pair(v);
+  v = GS > 16 ? fmaxf(p.x, p.y) : v;
+  p = sf_swap32_pair(v);
+  return GS > 32 ? fmaxf(p.x, p.y) : v;
+}
+__device__ __forceinline__ float sf_group_tree_sum(float v, int GS) {
+  float t = v + sf_dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+  v = GS > 1 ? t : v;
+  t = v + sf_dpp<0x4E>(v);        // quad_perm [2,3,0,1]
+  v = GS > 2 ? t : v;
+  t = v + sf_dpp<0x141>(v);       // row_half_mirror
+  v = GS > 4 ? t : v;
+  t = v + sf_dpp<0x140>(v);       // row_mirror
+  v = GS > 8 ? t : v;
+  float2_t p = sf_swap16_pair(v);
+  v = GS > 16 ? p.x + p.y : v;
+  p = sf_swap32_pair(v);
+  return GS > 32 ? p.x + p.y : v;
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the same bits (each step
 // adds a value and its butterfly partner, and fp addition commutes).
 __device__ __forceinline__ float sf_wave_sum(float v) {

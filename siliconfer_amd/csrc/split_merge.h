@@ -7,8 +7,14 @@
 // The output row is
 //   M = max_s m_s,  w_s = 2^(m_s - M),  out = (sum_s w_s acc_s) / (sum_s w_s l_s),
 // the reference's combine (/root/reference/siliconfer/kernels/metal/
-// q4_attention.py:63-70, 256-261, there in base e), with both sums taken in split
-// order by fmaf, so every consumer of the partials computes the same bits.
+// q4_attention.py:63-70, 256-261, there in base e). Both sums run over the
+// fp32 products w_s acc_s and w_s l_s, each rounded on its own, as a pairwise
+// tree: over the indices [0, P), P the smallest power of two >= S, terms at
+// s >= S being +0, the first level adds the pairs (2i, 2i + 1), every next
+// level the pairs of the level before. A consumer evaluates that tree in
+// registers (sf_tree_sum) or across P lanes with xor butterflies (the two
+// lanes of a pair add the same two values), so every consumer of the
+// partials computes the same bits.
 // An empty split (no tokens) has m = -inf, l = 0, acc = 0 and weighs 0; a row
 // with no tokens at all comes out as zeros.
 //
@@ -34,6 +40,32 @@ __device__ __forceinline__ float sf_merge_mref(float M) { return M == -INFINITY 
 // The weight 2^(m_s - M) of one split (exp2(-inf) = 0 for an empty split).
 __device__ __forceinline__ float sf_merge_weight(float m, float mref) {
   return __builtin_amdgcn_exp2f(m - mref);
+}
+
+// One term of a sum: the rounded product x w (never contracted with the
+// tree's adds into an fma: the multiply carries no contraction flag).
+__device__ __forceinline__ float sf_merge_term(float x, float w) {
+#pragma clang fp contract(off)
+  return x * w;
+}
+
+// The tree's span: the smallest power of two >= S.
+__host__ __device__ inline int sf_merge_span(int S) {
+  int P = 1;
+  while (P < S) P <<= 1;
+  return P;
+}
+
+// The pairwise tree over t[0, P) (P a power of two <= N; t[s] = +0 past the
+// terms): t[0] on return. Entries at or past P are left unused.
+template <int N>
+__device__ __forceinline__ float sf_tree_sum(float (&t)[N], int P) {
+#pragma unroll
+  for (int off = 1; off < N; off <<= 1)
+#pragma unroll
+    for (int i = 0; i < N; i += 2 * off)
+      if (off < P) t[i] = t[i] + t[i + off];
+  return t[0];
 }
 
 // The merged value from the weighted sums, as a rounded fp32 product (opaque,
