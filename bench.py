@@ -58,7 +58,6 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -358,29 +357,15 @@ def _config4(dev, lib, timer, cur, out, T):
     nsp = lib.sf_attn_default_splits_d(1, 2, T, 64)
     ws_bytes = lib.sf_attn_workspace_bytes(1, 14, 64, nsp)
     wsp = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)  # split partials
-    fw_bytes = lib.sf_attn_fused_workspace_bytes(1, 14, 64, nsp)
-    fws = torch.zeros(fw_bytes, dtype=torch.uint8, device=dev)  # zeroed once, as the call requires
-    one = [(lambda a=a: lib.sf_attn_decode_i8kv_fused(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
-                                                      a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
-                                                      1, fws.data_ptr(), fw_bytes, 1, 14, 2, T, T, 64,
-                                                      0.125, nsp, 0, -1, cur())) for a in sets]
-    two = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
+    fns = [(lambda a=a: lib.sf_attn_decode_i8kv(q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(),
                                                 a[2].data_ptr(), a[3].data_ptr(), 1, o.data_ptr(),
                                                 1, wsp.data_ptr(), ws_bytes, 1, 14, 2, T, T, 64,
                                                 0.125, nsp, cur())) for a in sets]
-    us = timer.per_call_us(one)
-    us2 = timer.per_call_us(two)
-    err = ctypes.c_int(-1)
-    _lib_check = lib.sf_attn_fused_error(fws.data_ptr(), ctypes.addressof(err), cur())
-    if _lib_check != 0 or err.value != 0:
-        raise RuntimeError(f"sf_attn_decode_i8kv_fused: error word {err.value}")
+    us = timer.per_call_us(fns)
     nb = 2 * 2 * T * 64 + 2 * 2 * 2 * T + 2 * 2 * 14 * 64
     out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
                                  "bytes": nb, "splits": nsp,
-                                 "launches": "one" if nsp == 1 else
-                                 "one (sf_attn_decode_i8kv_fused: split partials as tagged words, "
-                                 "merged in the same launch)",
-                                 "two_launch_us": round(us2, 3)}
+                                 "launches": "one" if nsp == 1 else "two (split partials, merge)"}
 
 
 def sweep_attn_splits(dev, head_dim=64, Ts=(128, 512, 1024, 4096, 16384),

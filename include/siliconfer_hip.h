@@ -191,8 +191,8 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
  * 512). D <= 256 (the reference's bound, q4_attention.py:78,227-228) and
  * D % 8 == 0. One split is one launch; more splits write their partials
  * (m, l, acc) to the workspace and a second launch merges them with the
- * reference's combine rule (q4_attention.py:63-70, 256-261), the splits in
- * order.
+ * reference's combine rule (q4_attention.py:63-70, 256-261), each sum a
+ * pairwise tree over the splits in order.
  * workspace: sf_attn_workspace_bytes(B, H, D, n_splits) bytes, 256-byte
  * aligned (NULL for one split), no initial contents needed: acc
  * [B*H][n_splits][D] fp32 at offset 0, then (m, l) [B*H][n_splits][2] fp32
@@ -211,30 +211,6 @@ int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const
                         int out_dtype, void *workspace, size_t workspace_bytes, int B, int H,
                         int KVH, int T, int T_cap, int D, float scale, int n_splits,
                         void *stream);
-
-/* sf_attn_decode_i8kv as one launch (same reference interface,
- * q4_attention.py:200-261, same result bit for bit): each split publishes its
- * partial as tagged words (value, launch tag) and then merges a slice of its
- * (b, kv head)'s outputs from every split's words, polling until all carry
- * the launch's tag; the tag comes from a per-(b, kv head) counter in the
- * workspace that the call advances. Shapes outside the one-launch kernel
- * (one split, the VALU kernel's shapes, grids over 256 workgroups, merge
- * slices over 2048 words) take the two launches, in the same workspace.
- * workspace: sf_attn_fused_workspace_bytes(B, H, D, n_splits) bytes, 256-byte
- * aligned, ZEROED before its first use (each call leaves it valid for the
- * next); calls that share it must not overlap. spin_cap: poll rounds before a
- * workgroup gives up (<= 0: 2^20); a workgroup that gives up writes NaN
- * outputs and sets the error word, which sf_attn_fused_error reads
- * (synchronously; 0: none). drop_split: a test hook, that split publishes
- * nothing (-1: none). */
-size_t sf_attn_fused_workspace_bytes(int B, int H, int D, int n_splits);
-int sf_attn_decode_i8kv_fused(const void *q, int q_dtype, const int8_t *k_codes,
-                              const void *k_scales, const int8_t *v_codes, const void *v_scales,
-                              int scale_dtype, void *out, int out_dtype, void *workspace,
-                              size_t workspace_bytes, int B, int H, int KVH, int T, int T_cap,
-                              int D, float scale, int n_splits, int spin_cap, int drop_split,
-                              void *stream);
-int sf_attn_fused_error(const void *workspace, int *err, void *stream);
 
 /* No counterpart in the reference: sf_attn_decode_i8kv for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that

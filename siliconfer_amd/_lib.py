@@ -61,11 +61,6 @@ _SIGS = {
     "sf_attn_decode_i8kv": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                    _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f,
                                    _c_i, _c_p]),
-    "sf_attn_fused_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i]),
-    "sf_attn_decode_i8kv_fused": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
-                                         _c_p, _c_sz, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f,
-                                         _c_i, _c_i, _c_i, _c_p]),
-    "sf_attn_fused_error": (_c_i, [_c_p, _c_p, _c_p]),
     "sf_attn_noalloc_max_bytes": (_c_sz, []),
     "sf_attn_decode_i8kv_noalloc": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i,
                                            _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_p]),

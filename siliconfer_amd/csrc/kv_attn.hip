@@ -454,174 +454,13 @@ __device__ __forceinline__ float sum_x16_x32(float v) {
   return p.x + p.y;
 }
 
-// The one-launch split attention (FUSE): each split publishes its partial as
-// tagged words, (fp32 bits, tag) in one 8-byte store, and then merges a slice
-// of its (b, kv head)'s outputs from every split's words, polling until all
-// carry this launch's tag (no counter, no wait for store acknowledgements).
-// The tag is the group's epoch word + 1; split 0 stores the new epoch once it
-// has seen every split's words, i.e. after every workgroup of the group read
-// the old one. Polls are bounded: past spin_cap rounds the workgroup records
-// an error word and writes NaN outputs, so every wave exits.
-struct FuseArgs {
-  uint64_t *acc_ll;   // [B*H][S][D] (value bits, tag)
-  uint64_t *ml_ll;    // [B*H][S][2] (m, l)
-  uint32_t *epoch;    // [B*KVH] launch counter of each (b, kv head) group
-  int *err;           // 0, or 1 after a poll gave up
-  int spin_cap;       // poll rounds before giving up
-  int drop_split;     // host test hook: this split publishes nothing (-1: none)
-};
-constexpr int kFuseItems = 8;         // tagged words one thread polls
-constexpr int kFuseMaxGroups = 1024;  // (b, kv head) epoch words
-constexpr int kFuseMaxGrid = 256;     // workgroups: at most one per CU, all resident together
-constexpr size_t kFuseHeaderBytes = 256 + 4 * kFuseMaxGroups;  // err word, then the epochs
-
-__device__ __forceinline__ uint64_t fz_load(const uint64_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void fz_store(uint64_t *p, float v, uint32_t tag) {
-  __hip_atomic_store(p, (uint64_t)sf_bitcast<uint32_t>(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// LDS exchange barrier of the fused merge: this wave's LDS accesses done, then
-// s_barrier (a __syncthreads would also wait for the partial's stores)
-#define ATT_BARRIER()                                  \
-  do {                                                 \
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); \
-    __builtin_amdgcn_s_barrier();                      \
-    asm volatile("" ::: "memory");                     \
-  } while (0)
-
-// The merge role of a FUSE workgroup: outputs [o0, o1) of its group's G * D
-// (o = h D + d), o0 = split * ceil(G D / S). Its threads poll the tagged words
-// those outputs need, every split's acc[h][d] and (m, l) of the heads covered,
-// into LDS (each thread until its own words carry `tag`); then the outputs are
-// combined with the rule of split_merge.h (the merge launch's arithmetic, so
-// the same bits): P lanes per output (the tree's span, P <= 64), lane g
-// holding split g, two outputs per lane, the max, the weights, the terms and
-// the tree's levels across the P lanes.
-template <int D, int NT>
-__device__ __forceinline__ void attn_fuse_merge(const FuseArgs &fz, float *smem, uint32_t tag, int split,
-                                                int S, int G, size_t bh0, int grp, void *out, int odt,
-                                                int tid) {
-  const int GD = G * D;
-  const int per = (GD + S - 1) / S;
-  const int o0 = min(split * per, GD), o1 = min(o0 + per, GD);
-  const int nout = o1 - o0;
-  const int h0 = o0 / D;
-  const int nh = nout > 0 ? (o1 - 1) / D - h0 + 1 : 0;
-  const int nacc = nout * S, nitems = nacc + nh * S * 2;
-  float *va = smem;            // [S][per] acc values (a split's outputs side by side)
-  float *vm = smem + per * S;  // [nh][S][2] (m, l)
-  // q / n for 0 <= q < 2^16, 1 <= n <= 2^8 through an fp32 reciprocal: the
-  // quotient's fraction lies in [0.5 / n, 1 - 0.5 / n], far wider than the
-  // reciprocal's error, so the truncation is exact (integer division would
-  // cost ~40 instructions)
-  const float rS = 1.f / (float)S, r2S = 0.5f * rS;
-  auto div = [](int q, float rn) { return (int)(((float)q + 0.5f) * rn); };
-  // item idx: its word and its LDS slot
-  auto item = [&](int idx, const uint64_t *&p, int &li) {
-    if (idx < nacc) {
-      const int ol = div(idx, rS), sp = idx - ol * S;
-      const int o = o0 + ol, h = o / D, d = o - h * D;
-      p = fz.acc_ll + ((bh0 + h) * S + sp) * D + d;
-      li = sp * per + ol;
-    } else {
-      const int j = idx - nacc, hh = div(j, r2S), r = j - hh * 2 * S;
-      p = fz.ml_ll + ((bh0 + h0 + hh) * S + (r >> 1)) * 2 + (r & 1);
-      li = per * S + hh * 2 * S + r;
-    }
-  };
-  __shared__ int gave_up;
-  if (tid == 0) gave_up = 0;
-  ATT_BARRIER();  // every wave is done with the wave states in smem
-  // each thread polls its own words until all carry the tag (no workgroup
-  // vote per round: a thread stops as soon as its words are in)
-  uint32_t pend = 0;
-  const uint64_t *ip[kFuseItems];
-  int il[kFuseItems];
-#pragma unroll
-  for (int k = 0; k < kFuseItems; ++k) {
-    const int idx = max(0, min(tid + NT * k, nitems - 1));  // unused when past nitems
-    item(idx, ip[k], il[k]);
-    if (tid + NT * k < nitems) pend |= 1u << k;
-  }
-  for (int round = 0; pend; ++round) {
-    if (round == fz.spin_cap) {
-      gave_up = 1;
-      __hip_atomic_store(fz.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    uint64_t w[kFuseItems];
-#pragma unroll
-    for (int k = 0; k < kFuseItems; ++k) {
-      w[k] = 0;
-      if (pend >> k & 1) w[k] = fz_load(ip[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < kFuseItems; ++k) {
-      if ((pend >> k & 1) && (uint32_t)(w[k] >> 32) == tag) {
-        smem[il[k]] = sf_bitcast<float>((uint32_t)w[k]);
-        pend &= ~(1u << k);
-      }
-    }
-    if (pend) __builtin_amdgcn_s_sleep(1);
-  }
-  ATT_BARRIER();  // every thread's words are in LDS (or some thread gave up)
-  const bool timed_out = gave_up != 0;
-  // split 0 has seen every split's words: each of them read the old epoch
-  if (split == 0 && tid == 0) __hip_atomic_store(fz.epoch + grp, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int P = sf_merge_span(S);
-  const int opp = NT / P;
-  const int g = tid % P;
-  const bool in = g < S;
-  const int sc = min(g, S - 1);
-  constexpr int U = 2;
-  for (int ob = 0; ob < nout; ob += U * opp) {
-    int olr[U], ol[U];
-    float mk[U], M[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      olr[u] = ob + u * opp + tid / P;
-      ol[u] = min(olr[u], nout - 1);
-      const int h = (o0 + ol[u]) / D;
-      mk[u] = in ? vm[(h - h0) * 2 * S + 2 * sc] : -INFINITY;
-      M[u] = sf_group_tree_max(mk[u], P);
-    }
-    float tv[U], tl[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int h = (o0 + ol[u]) / D;
-      const float w = in ? sf_merge_weight(mk[u], sf_merge_mref(M[u])) : 0.f;
-      tv[u] = in ? sf_merge_term(va[sc * per + ol[u]], w) : 0.f;
-      tl[u] = in ? sf_merge_term(vm[(h - h0) * 2 * S + 2 * sc + 1], w) : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      tv[u] = sf_group_tree_sum(tv[u], P);
-      tl[u] = sf_group_tree_sum(tl[u], P);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (g == 0 && olr[u] < nout) {
-        const int o = o0 + ol[u], h = o / D, d = o - h * D;
-        const float r = timed_out ? __builtin_nanf("") : sf_merge_finish(tl[u], tv[u]);
-        const size_t e = (bh0 + h) * D + d;
-        if (odt == SF_F32) ((float *)out)[e] = r;
-        else if (odt == SF_F16) ((f16 *)out)[e] = (f16)r;
-        else ((uint16_t *)out)[e] = sf_f32_to_bf16(r);
-      }
-    }
-  }
-}
-
-template <int QDT, int SDT, int D, int NW, int NB, bool FUSE = false>
+template <int QDT, int SDT, int D, int NW, int NB>
 __global__ void __launch_bounds__(NW * 64)
 k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const void *__restrict__ ks,
             const int8_t *__restrict__ vc, const void *__restrict__ vs, float *part_acc,
             float *part_ml, void *__restrict__ out, int odt, int H, int KVH,
             int T, const int *__restrict__ T_dev, int causal, int T_cap, float qscale,
-            int n_splits, int vscale, FuseArgs fz) {
+            int n_splits, int vscale) {
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(NW == kAttnWaves || NW == 8 || NW == 16, "4 waves (split-T), 8 or 16 (one split)");
   constexpr int NT = NW * 64;
@@ -746,10 +585,6 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
     if (32 * (j0 + jstep * u) < T_cap) load(j0 + jstep * u, tl[u]);
     if (u == 0 && T_dev) tdev = __hip_atomic_load(T_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // the group's epoch, behind the tiles (read only when the partial is published)
-  const int grp = b * KVH + kvh;
-  uint32_t epoch = 0;
-  if constexpr (FUSE) epoch = __hip_atomic_load(fz.epoch + grp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("" : "+v"(tdev));  // read here, not right behind its load
   int Tv = T_dev ? tdev + T : T;
   if (causal) Tv = (T_dev ? tdev : T) + b + 1;
@@ -859,9 +694,6 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
   __syncthreads();
   const bool single = n_splits == 1;
   constexpr int NQ = D / 4;
-  asm volatile("" : "+v"(epoch));
-  const uint32_t tag = epoch + 1u;
-  const bool publish = !FUSE || split != fz.drop_split;
   for (int it = tid; it < G * NQ; it += NT) {
     const int h = it / NQ, d4 = (it - h * NQ) * 4;
     float M = -INFINITY;
@@ -886,23 +718,11 @@ k_attn_mfma(const void *__restrict__ q, const int8_t *__restrict__ kc, const voi
         else if (odt == SF_F16) ((f16 *)out)[o + i] = (f16)v;
         else ((uint16_t *)out)[o + i] = sf_f32_to_bf16(v);
       }
-    } else if constexpr (FUSE) {
-      if (publish) {
-        uint64_t *pa = fz.acc_ll + ((bh0 + h) * n_splits + split) * D + d4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) fz_store(pa + i, a[i], tag);
-        if (d4 == 0) {
-          uint64_t *pm = fz.ml_ll + ((bh0 + h) * n_splits + split) * 2;
-          fz_store(pm, M, tag);
-          fz_store(pm + 1, L, tag);
-        }
-      }
     } else {
       *(float4_t *)(part_acc + ((bh0 + h) * n_splits + split) * D + d4) = a;
       if (d4 == 0) *(float2_t *)(part_ml + ((bh0 + h) * n_splits + split) * 2) = float2_t{M, L};
     }
   }
-  if constexpr (FUSE) attn_fuse_merge<D, NT>(fz, smem, tag, split, n_splits, G, bh0, grp, out, odt, tid);
 }
 
 int pow2_log2_at_least(int v) {
@@ -1199,96 +1019,53 @@ extern "C" int sf_kv_quant_append(const void *k_new, const void *v_new, int in_d
 
 namespace {
 
-// Merge launch of a split-T call: one lane per output element (row bh, dim d),
-// the splits combined with the rule of split_merge.h (pairwise trees). Up to
-// kMergeLoadSplits splits, every load of the element goes out before the
-// first use; longer rows take M in a first pass, then the sums in chunks of
-// kMergeLoadSplits splits whose loads go out together (a loop of one split
-// per trip leaves each load's latency exposed), each chunk a full subtree.
-constexpr int kMergeLoadSplits = 64;
-constexpr int kMergeThreads = 64;
+// Merge launch of a split-T call, with the rule of split_merge.h: GS lanes
+// per output element (row bh, dim d), GS = the tree's span P up to 64; lane g
+// loads the (m, l, acc) of splits [g SPL, (g + 1) SPL), SPL = P / GS, and
+// sums that block's subtree in registers; the max and the tree's upper
+// levels run across the lanes (every load of a lane in flight at once, no
+// lane walking the splits one by one).
+constexpr int kMergeThreads = 256;
 
+template <int SPL>
 __global__ void __launch_bounds__(kMergeThreads)
 k_attn_merge(const float *__restrict__ acc, const float *__restrict__ ml, void *__restrict__ out,
              int odt, int rows, int D, int S) {
   // every argument fetched in one round at entry (the compiler would split them)
   asm volatile("" ::"s"(acc), "s"(ml), "s"(out), "s"(odt), "s"(rows), "s"(D), "s"(S));
-  constexpr int C = kMergeLoadSplits;
-  const int e = blockIdx.x * kMergeThreads + threadIdx.x;
-  if (e >= rows * D) return;
-  const int bh = e / D, d = e - bh * D;
+  const int P = sf_merge_span(S), GS = P / SPL;
+  const int e = blockIdx.x * (kMergeThreads / GS) + threadIdx.x / GS, g = threadIdx.x % GS;
+  const int n = rows * D, ec = min(e, n - 1);  // lanes past the last output compute, then drop
+  const int bh = ec / D, d = ec - bh * D;
   const float2_t *mlr = (const float2_t *)ml + (size_t)bh * S;
   const float *ar = acc + (size_t)bh * S * D + d;
-  float L, v;
-  if (S <= C) {
-    float2_t mv[C];
-    float av[C];
+  float mv[SPL], lv[SPL], av[SPL];
+  float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < C; ++j)
-      if (j < S) {
-        mv[j] = mlr[j];
-        av[j] = ar[(size_t)j * D];
-      }
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < C; ++j)
-      if (j < S) M = fmaxf(M, mv[j].x);
-    const float mref = sf_merge_mref(M);
-    float tl[C];
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-      const float w = j < S ? sf_merge_weight(mv[j].x, mref) : 0.f;
-      tl[j] = j < S ? sf_merge_term(mv[j].y, w) : 0.f;
-      av[j] = j < S ? sf_merge_term(av[j], w) : 0.f;
-    }
-    const int P = sf_merge_span(S);
-    L = sf_tree_sum(tl, P);
-    v = sf_tree_sum(av, P);
-  } else {  // chunks of C splits, each chunk's loads in flight together; each
-            // chunk a full subtree, then the tree over the chunk sums
-    constexpr int NC = kMaxSplits / C;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < S; s0 += C) {
-      float mc[C];
-#pragma unroll
-      for (int j = 0; j < C; ++j) mc[j] = s0 + j < S ? mlr[s0 + j].x : -INFINITY;
-#pragma unroll
-      for (int j = 0; j < C; ++j) M = fmaxf(M, mc[j]);
-    }
-    const float mref = sf_merge_mref(M);
-    float cl[NC], cv[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) cl[c] = cv[c] = 0.f;
-    for (int c = 0; c * C < S; ++c) {
-      const int s0 = c * C;
-      float2_t mv[C];
-      float av[C], tl[C];
-#pragma unroll
-      for (int j = 0; j < C; ++j)
-        if (s0 + j < S) {
-          mv[j] = mlr[s0 + j];
-          av[j] = ar[(size_t)(s0 + j) * D];
-        }
-#pragma unroll
-      for (int j = 0; j < C; ++j) {
-        const bool in = s0 + j < S;
-        const float w = in ? sf_merge_weight(mv[j].x, mref) : 0.f;
-        tl[j] = in ? sf_merge_term(mv[j].y, w) : 0.f;
-        av[j] = in ? sf_merge_term(av[j], w) : 0.f;
-      }
-      const float cls = sf_tree_sum(tl, C), cvs = sf_tree_sum(av, C);
-#pragma unroll
-      for (int k = 0; k < NC; ++k)
-        if (k == c) cl[k] = cls, cv[k] = cvs;
-    }
-    const int P = sf_merge_span(S) / C;
-    L = sf_tree_sum(cl, P);
-    v = sf_tree_sum(cv, P);
+  for (int k = 0; k < SPL; ++k) {
+    const int sp = g * SPL + k, sc = min(sp, S - 1);
+    const float2_t m = mlr[sc];
+    mv[k] = sp < S ? m.x : -INFINITY;
+    lv[k] = m.y;
+    av[k] = ar[(size_t)sc * D];
+    mx = fmaxf(mx, mv[k]);
   }
-  const float r = sf_merge_finish(L, v);
-  if (odt == SF_F32) ((float *)out)[e] = r;
-  else if (odt == SF_F16) ((f16 *)out)[e] = (f16)r;
-  else ((uint16_t *)out)[e] = sf_f32_to_bf16(r);
+  const float mref = sf_merge_mref(sf_group_tree_max(mx, GS));
+#pragma unroll
+  for (int k = 0; k < SPL; ++k) {
+    const bool in = g * SPL + k < S;
+    const float w = in ? sf_merge_weight(mv[k], mref) : 0.f;
+    av[k] = in ? sf_merge_term(av[k], w) : 0.f;
+    lv[k] = in ? sf_merge_term(lv[k], w) : 0.f;
+  }
+  const float v = sf_group_tree_sum(sf_tree_sum(av, SPL), GS);
+  const float L = sf_group_tree_sum(sf_tree_sum(lv, SPL), GS);
+  if (g == 0 && e < n) {
+    const float r = sf_merge_finish(L, v);
+    if (odt == SF_F32) ((float *)out)[e] = r;
+    else if (odt == SF_F16) ((f16 *)out)[e] = (f16)r;
+    else ((uint16_t *)out)[e] = sf_f32_to_bf16(r);
+  }
 }
 
 }  // namespace
@@ -1338,8 +1115,12 @@ static int attn_merge_launch(const char *what, const float *part_acc, const floa
                              int merge) {
   if (n_splits > 1 && merge) {
     const int n = rows * D;
-    k_attn_merge<<<(n + kMergeThreads - 1) / kMergeThreads, kMergeThreads, 0, st>>>(
-        part_acc, part_ml, out, odt, rows, D, n_splits);
+    const int P = sf_merge_span(n_splits), spl = P > 64 ? P / 64 : 1, per_block = kMergeThreads / (P / spl);
+    const unsigned grid = (unsigned)((n + per_block - 1) / per_block);
+    if (spl == 1) k_attn_merge<1><<<grid, kMergeThreads, 0, st>>>(part_acc, part_ml, out, odt, rows, D, n_splits);
+    else if (spl == 2) k_attn_merge<2><<<grid, kMergeThreads, 0, st>>>(part_acc, part_ml, out, odt, rows, D, n_splits);
+    else if (spl == 4) k_attn_merge<4><<<grid, kMergeThreads, 0, st>>>(part_acc, part_ml, out, odt, rows, D, n_splits);
+    else k_attn_merge<8><<<grid, kMergeThreads, 0, st>>>(part_acc, part_ml, out, odt, rows, D, n_splits);
   }
   return sf_check_launch(what);
 }
@@ -1351,7 +1132,7 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
                        int scale_dtype, void *out, int out_dtype, void *workspace,
                        size_t workspace_bytes, int B, int H, int KVH, int T, const int *T_dev,
                        int causal, int T_cap, int D, float scale, int n_splits, void *stream,
-                       int merge = 1, const FuseArgs *fuse = nullptr) {
+                       int merge = 1) {
   SF_REQUIRE(H % KVH == 0, SF_EINVAL, "n_heads=%d not a multiple of n_kv_heads=%d", H, KVH);
   SF_REQUIRE(D <= kMaxD, SF_EINVAL, "head_dim=%d exceeds kernel's compile-time max 256", D);
   SF_REQUIRE(D % 8 == 0, SF_EUNSUPPORTED, "head_dim=%d: need a multiple of 8", D);
@@ -1388,34 +1169,23 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
   if (mfma_ok && G <= 16 && (D == 64 || D == 128) && n_splits <= kMfmaMaxSplits &&
       (((uintptr_t)k_codes | (uintptr_t)v_codes) & 15) == 0) {
     dim3 grid(n_splits, KVH, B);
-    // one launch (partials published as tagged words, merged in place) when
-    // the grid is resident at once and a workgroup's merge slice fits its polls
-    const int fz_per = (G * D + n_splits - 1) / n_splits;
-    const int fz_items = fz_per * n_splits + ((fz_per + D - 1) / D + 1) * n_splits * 2;
-    const bool fused = fuse && n_splits > 1 && n_splits * KVH * B <= kFuseMaxGrid &&
-                       B * KVH <= kFuseMaxGroups && sf_merge_span(n_splits) <= 64 &&
-                       fz_items <= kFuseItems * kAttnThreads;
-    const FuseArgs fzv = fused ? *fuse : FuseArgs{nullptr, nullptr, nullptr, nullptr, 0, -1};
     // scale loads in aligned groups of 4 tokens when every row start allows it
     const size_t sal = scale_dtype == SF_F16 ? 8 : 16;
     const int vscale = T_cap % 4 == 0 && (uintptr_t)k_scales % sal == 0 &&
                        (uintptr_t)v_scales % sal == 0;
-#define SF_MFMA_LAUNCH(QD, SD, DD, NWV, NBV, FZ)                                                 \
-  k_attn_mfma<QD, SD, DD, NWV, NBV, FZ><<<grid, NWV * 64, 0, st>>>(                              \
+#define SF_MFMA_LAUNCH(QD, SD, DD, NWV, NBV)                                                     \
+  k_attn_mfma<QD, SD, DD, NWV, NBV><<<grid, NWV * 64, 0, st>>>(                                  \
       q, k_codes, k_scales, v_codes, v_scales, part_acc, part_ml, out, out_dtype, H,   \
-      KVH, T, T_dev, causal, T_cap, qscale, n_splits, vscale, fzv)
-#define SF_MFMA_D(QD, SD)                                                \
-  do {                                                                   \
-    if (n_splits == 1) {                                                 \
-      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, 16, 1, false);             \
-      else SF_MFMA_LAUNCH(QD, SD, 128, 8, 2, false);                     \
-    } else if (fused) {                                                  \
-      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, kAttnWaves, 2, true);      \
-      else SF_MFMA_LAUNCH(QD, SD, 128, kAttnWaves, 2, true);             \
-    } else {                                                             \
-      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, kAttnWaves, 2, false);     \
-      else SF_MFMA_LAUNCH(QD, SD, 128, kAttnWaves, 2, false);            \
-    }                                                                    \
+      KVH, T, T_dev, causal, T_cap, qscale, n_splits, vscale)
+#define SF_MFMA_D(QD, SD)                                   \
+  do {                                                      \
+    if (n_splits == 1) {                                    \
+      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, 16, 1);       \
+      else SF_MFMA_LAUNCH(QD, SD, 128, 8, 2);               \
+    } else {                                                \
+      if (D == 64) SF_MFMA_LAUNCH(QD, SD, 64, kAttnWaves, 2); \
+      else SF_MFMA_LAUNCH(QD, SD, 128, kAttnWaves, 2);      \
+    }                                                       \
   } while (0)
     if (scale_dtype == SF_F16) {
       if (q_dtype == SF_F32) SF_MFMA_D(SF_F32, SF_F16);
@@ -1428,7 +1198,6 @@ static int attn_launch(const char *what, const void *q, int q_dtype, const int8_
     }
 #undef SF_MFMA_D
 #undef SF_MFMA_LAUNCH
-    if (fused) return sf_check_launch(what);
     return attn_merge_launch(what, part_acc, part_ml, out, out_dtype, B * H, D, n_splits, st, merge);
   }
   const int HB = attn_heads_per_block(G);
@@ -1477,61 +1246,6 @@ extern "C" int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_c
   return attn_launch("sf_attn_decode_i8kv", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
                      scale_dtype, out, out_dtype, workspace, workspace_bytes, B, H, KVH, T,
                      nullptr, 0, T_cap, D, scale, n_splits, stream);
-}
-
-// Fused-call workspace: the error word at 0, the (b, kv head) epochs at 256,
-// then the tagged acc and (m, l) words, then a plain split workspace for the
-// shapes that take two launches.
-static size_t fuse_ws_parts(int B, int H, int D, int S, size_t *acc_off, size_t *ml_off,
-                            size_t *plain_off) {
-  const size_t n = (size_t)B * H * S;
-  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  *acc_off = al(kFuseHeaderBytes);
-  *ml_off = al(*acc_off + n * D * sizeof(uint64_t));
-  *plain_off = al(*ml_off + n * 2 * sizeof(uint64_t));
-  return *plain_off + sf_attn_workspace_bytes(B, H, D, S);
-}
-
-extern "C" size_t sf_attn_fused_workspace_bytes(int B, int H, int D, int n_splits) {
-  if (B <= 0 || H <= 0 || D <= 0 || n_splits <= 0) return 0;
-  if (n_splits > kMaxSplits) n_splits = kMaxSplits;
-  size_t a, m, p;
-  return fuse_ws_parts(B, H, D, n_splits, &a, &m, &p);
-}
-
-extern "C" int sf_attn_decode_i8kv_fused(const void *q, int q_dtype, const int8_t *k_codes,
-                                         const void *k_scales, const int8_t *v_codes,
-                                         const void *v_scales, int scale_dtype, void *out,
-                                         int out_dtype, void *workspace, size_t workspace_bytes,
-                                         int B, int H, int KVH, int T, int T_cap, int D,
-                                         float scale, int n_splits, int spin_cap, int drop_split,
-                                         void *stream) {
-  SF_REQUIRE(B > 0 && H > 0 && KVH > 0 && D > 0 && T >= 0 && T <= T_cap, SF_EINVAL,
-             "invalid attention shape B=%d H=%d KVH=%d T=%d T_cap=%d D=%d", B, H, KVH, T, T_cap, D);
-  SF_REQUIRE(workspace, SF_EINVAL, "null workspace");
-  SF_REQUIRE(((uintptr_t)workspace & 255) == 0, SF_EINVAL, "workspace must be 256-byte aligned");
-  if (n_splits <= 0) n_splits = sf_attn_default_splits_d(B, KVH, T, D);
-  n_splits = n_splits < (T > 0 ? T : 1) ? n_splits : (T > 0 ? T : 1);
-  if (n_splits > kMaxSplits) n_splits = kMaxSplits;
-  size_t acc_off, ml_off, plain_off;
-  const size_t need = fuse_ws_parts(B, H, D, n_splits, &acc_off, &ml_off, &plain_off);
-  SF_REQUIRE(workspace_bytes >= need, SF_EINVAL, "fused attention workspace too small: %zu < %zu",
-             workspace_bytes, need);
-  char *ws = (char *)workspace;
-  const FuseArgs fz{(uint64_t *)(ws + acc_off), (uint64_t *)(ws + ml_off), (uint32_t *)(ws + 256),
-                    (int *)ws, spin_cap > 0 ? spin_cap : (1 << 20), drop_split};
-  return attn_launch("sf_attn_decode_i8kv_fused", q, q_dtype, k_codes, k_scales, v_codes, v_scales,
-                     scale_dtype, out, out_dtype, ws + plain_off, workspace_bytes - plain_off, B, H,
-                     KVH, T, nullptr, 0, T_cap, D, scale, n_splits, stream, 1, &fz);
-}
-
-extern "C" int sf_attn_fused_error(const void *workspace, int *err, void *stream) {
-  SF_REQUIRE(workspace && err, SF_EINVAL, "null pointer argument");
-  hipStream_t st = (hipStream_t)stream;
-  if (hipMemcpyAsync(err, workspace, sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
-      hipStreamSynchronize(st) != hipSuccess)
-    return sf_fail(SF_EHIP, "sf_attn_fused_error: reading the error word failed");
-  return SF_OK;
 }
 
 extern "C" int sf_attn_decode_i8kv_dev(const void *q, int q_dtype, const int8_t *k_codes,

@@ -42,14 +42,12 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
-    """Attention workspace of the one-launch call (sf_attn_decode_i8kv_fused:
-    the split partials as tagged words and each (b, kv head)'s launch
-    counter), one per (device, stream), grown on demand. It starts zeroed, as
-    that call requires, and every call leaves it valid for the next."""
+    """Attention workspace (the split partials), one per (device, stream), grown
+    on demand; nothing in it needs clearing between calls."""
     key = (device, stream_handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -90,16 +88,16 @@ def attention_decode(q: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Ten
     if n_splits is None or n_splits <= 0:
         n_splits = default_splits(B, KVH, T, D)
     n_splits = max(1, min(int(n_splits), max(T, 1), 512))
-    ws_bytes = lib.sf_attn_fused_workspace_bytes(B, H, D, n_splits)
+    ws_bytes = lib.sf_attn_workspace_bytes(B, H, D, n_splits)
     st = _lib.stream(q)
     ws = workspace(q.device, st, ws_bytes)
     if out is None:
         out = torch.empty((B, H, D), dtype=out_dtype, device=q.device)
-    rc = lib.sf_attn_decode_i8kv_fused(q.data_ptr(), _lib.dt(q), k_codes.data_ptr(), ks.data_ptr(),
-                                       v_codes.data_ptr(), vs.data_ptr(), _lib.dt(ks), out.data_ptr(),
-                                       _lib.dt(out), ws.data_ptr(), ws.numel(), B, H, KVH, T, T_cap, D,
-                                       float(scale), n_splits, 0, -1, st)
-    _lib.check(rc, "sf_attn_decode_i8kv_fused")
+    rc = lib.sf_attn_decode_i8kv(q.data_ptr(), _lib.dt(q), k_codes.data_ptr(), ks.data_ptr(),
+                                 v_codes.data_ptr(), vs.data_ptr(), _lib.dt(ks), out.data_ptr(),
+                                 _lib.dt(out), ws.data_ptr(), ws.numel(), B, H, KVH, T, T_cap, D,
+                                 float(scale), n_splits, st)
+    _lib.check(rc, "sf_attn_decode_i8kv")
     return out
 
 

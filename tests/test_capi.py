@@ -143,14 +143,6 @@ def test_attention_validation_and_sizes():
     acc = 14 * 256 * 64 * 4  # split acc, then (m, l) at the next 256-byte boundary
     assert lib.sf_attn_workspace_bytes(1, 14, 64, 256) == acc + 14 * 256 * 2 * 4
     assert lib.sf_attn_workspace_bytes(1, 14, 64, 3) == 10752 + 14 * 3 * 2 * 4
-    # one-launch call: error word + 1024 epochs (4352 B), tagged acc (8 B per
-    # value) and (m, l) words, each at a 256-byte boundary, then the plain layout
-    tagged = 4352 + 14 * 32 * 64 * 8 + 14 * 32 * 2 * 8
-    assert lib.sf_attn_fused_workspace_bytes(1, 14, 64, 32) == tagged + lib.sf_attn_workspace_bytes(1, 14, 64, 32)
-    assert lib.sf_attn_fused_workspace_bytes(1, 14, 64, 0) == 0
-    rc = lib.sf_attn_decode_i8kv_fused(None, 0, None, None, None, None, 1, None, 0, None, 0,
-                                       1, 14, 2, 16, 16, 64, 0.1, 2, 0, -1, None)
-    assert rc == -1 and "null workspace" in _lib.last_error()
     rc = lib.sf_attn_decode_i8kv_partials_dev(None, 0, None, None, None, None, 1, None, 0, 1, 14, 2,
                                               None, 0, 16, 16, 64, 0.1, 1, None)
     assert rc == -1 and "null pointer" in _lib.last_error()
