@@ -200,10 +200,9 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
  * overlap (use one workspace per stream). */
 size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
 /* Default split count (the reference's _choose_n_tiles, q4_attention.py:183-197,
- * re-tuned for MI355X): one split up to 896 cached tokens at head_dim <= 64
- * and up to 320 above, then about 128 (head_dim <= 64) or 32 tokens per
- * split, 16 to 64 splits.
- * sf_attn_default_splits is the head_dim-64 rule. */
+ * re-tuned for MI355X): one split up to 160 cached tokens, then 32 tokens per
+ * split up to 1024 tokens and 64 above, 8 to 64 splits (any head_dim).
+ * sf_attn_default_splits is the same rule. */
 int sf_attn_default_splits(int B, int KVH, int T);
 int sf_attn_default_splits_d(int B, int KVH, int T, int D);
 int sf_attn_decode_i8kv(const void *q, int q_dtype, const int8_t *k_codes, const void *k_scales,

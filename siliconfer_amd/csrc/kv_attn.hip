@@ -1081,19 +1081,23 @@ extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
 }
 
 extern "C" int sf_attn_default_splits_d(int B, int KVH, int T, int D) {
-  // One split (one workgroup per kv head, no merge launch) up to 896 tokens at
-  // head_dim 64 and 320 at larger head dims; beyond, about 128 (head_dim 64) or
-  // 32 (larger) tokens per split, at least 16 and at most 64 splits. Measured
-  // on MI355X at 14 / 2 heads (us, one split / best split count):
-  //   head_dim 64:  T = 512: 6.6 / 7.9;  1024: 8.7 / 8.2 (16-32 splits);
-  //                 4096: 22.5 / 8.9 (32);  16384: 79.5 / 11.0 (64);
-  //   head_dim 128: T = 256: 7.8 / 8.6;  448: 9.9 / 8.8 (16);  1024: 14.7 / 8.9 (32);
-  //                 4096: 43.8 / 10.0 (64).
+  // One split (one workgroup per (b, kv head), no merge launch) up to 160
+  // tokens; beyond, 32 tokens per split up to 1024 cached tokens and 64 above,
+  // at least 8 and at most 64 splits. Measured on MI355X at 14 / 2 heads,
+  // graph-timed over cold caches (us, one split / the rule's count):
+  //   head_dim 64:  T = 128: 4.8 / 4.9;  256: 5.4 / 5.2 (8);  512: 6.4 / 5.6 (16);
+  //                 1024: 8.5 / 5.9 (32);  4096: 6.4 (64; 32: 6.6);  16384: 7.9 (64);
+  //   head_dim 128: T = 128: 5.6 / 5.9;  256: 6.7 / 6.1 (8);  512: 9.2 / 6.4 (16);
+  //                 2048: 20.8 / 7.1 (32);  4096: 7.9 (64).
+  // Eight waves per split workgroup (one tile each) instead of four measured
+  // no faster at 4096-16384 tokens.
   (void)B;
   (void)KVH;
-  if (T <= (D <= 64 ? 896 : 320)) return 1;
-  int s = D <= 64 ? (T + 127) / 128 : (T + 31) / 32;
-  if (s < 16) s = 16;
+  (void)D;
+  if (T <= 160) return 1;
+  const int tps = T <= 1024 ? 32 : 64;
+  int s = (T + tps - 1) / tps;
+  if (s < 8) s = 8;
   if (s > 64) s = 64;
   return s;
 }

@@ -153,13 +153,13 @@ def test_attention_validation_and_sizes():
                                  1, 14, 3, 16, 16, 64, 0.1, 1, None)
     assert rc == -1 and "not a multiple" in _lib.last_error()
     assert lib.sf_attn_default_splits(1, 2, 16384) == 64
-    assert lib.sf_attn_default_splits(1, 2, 4096) == 32
+    assert lib.sf_attn_default_splits(1, 2, 4096) == 64
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
-    assert lib.sf_attn_default_splits(1, 2, 896) == 1 and lib.sf_attn_default_splits(1, 2, 897) == 16
-    assert lib.sf_attn_default_splits_d(1, 2, 896, 64) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 320, 128) == 1
-    assert lib.sf_attn_default_splits_d(1, 2, 321, 128) == 16
+    assert lib.sf_attn_default_splits(1, 2, 160) == 1 and lib.sf_attn_default_splits(1, 2, 161) == 8
+    assert lib.sf_attn_default_splits_d(1, 2, 512, 64) == 16
     assert lib.sf_attn_default_splits_d(1, 2, 1024, 128) == 32
+    assert lib.sf_attn_default_splits_d(1, 2, 1025, 128) == 17
+    assert lib.sf_attn_default_splits_d(1, 2, 2048, 64) == 32
     assert lib.sf_attn_default_splits_d(1, 2, 4096, 128) == 64
 
 
