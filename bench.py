@@ -339,6 +339,12 @@ def _config2(dev, lib, timer, cur, rng, out, N, K, W):
     out[f"config2_gemm_asym_m512_{N}x{K}"] = {
         "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
         "mfma_frac_of_bf16_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    if wsb:  # split K: the GEMM launch alone (its partials), timed the same way
+        part = [(lambda b=b: lib.sf_q4_gemm_partials(b.data_ptr(), X.data_ptr(), 2, 512, N, K, 64, 1,
+                                                     ws.data_ptr(), wsb, cur())) for b in blobs]
+        up = timer.per_call_us(part, reps=2)
+        out[f"config2_gemm_asym_m512_{N}x{K}"].update(
+            gemm_launch_us=round(up, 3), reduce_launch_us_by_difference=round(us - up, 3))
 
 
 def _config4(dev, lib, timer, cur, out, T):
@@ -366,6 +372,14 @@ def _config4(dev, lib, timer, cur, out, T):
     out[f"config4_attn_T{T}"] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
                                  "bytes": nb, "splits": nsp,
                                  "launches": "one" if nsp == 1 else "two (split partials, merge)"}
+    if nsp > 1:  # the split launch alone (partials, no merge), timed the same way
+        t0 = torch.zeros((1,), dtype=torch.int32, device=dev)
+        part = [(lambda a=a: lib.sf_attn_decode_i8kv_partials_dev(
+            q.data_ptr(), 1, a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(), 1,
+            wsp.data_ptr(), ws_bytes, 1, 14, 2, t0.data_ptr(), T, T, T, 64, 0.125, nsp, cur())) for a in sets]
+        up = timer.per_call_us(part)
+        out[f"config4_attn_T{T}"].update(split_launch_us=round(up, 3),
+                                         merge_launch_us_by_difference=round(us - up, 3))
 
 
 def sweep_attn_splits(dev, head_dim=64, Ts=(128, 512, 1024, 4096, 16384),
@@ -1032,6 +1046,7 @@ def summarize_e2e(trace_csv: str, steps: int = 16) -> dict:
 
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
     starts = [i for i, r in enumerate(rows) if "k_embed" in r["Kernel_Name"]]
+    steps = min(steps, len(starts) - 1)  # the first k_embed is the prompt's
     dec = rows[starts[-steps]:]
     per = {}
     for r in dec:
