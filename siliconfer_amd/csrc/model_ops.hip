@@ -183,6 +183,17 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+// Ordering of the last-block fold, stated for the hardware (the atomics are
+// relaxed, so C++ ordering alone would allow the count to pass the partials):
+// every partial is an agent-scope atomic store, which writes through to the
+// device-coherent level; s_waitcnt(0) returns only after the storing wave's
+// stores are acknowledged there, and the workgroup barrier (where used) puts
+// every wave's wait before tid 0's count increment. The block that takes the
+// last count therefore reads, with agent-scope atomic loads (which bypass the
+// non-coherent caches), partials that were all acknowledged before any count
+// that preceded its own. An acq_rel increment would add an L2 write-back per
+// block (agent-scope release on gfx950) for stores already written through.
+//
 // NORM: x is the fp32 residual row and the block applies the final RMSNorm
 // itself (sf_row_inv_rms, then x * inv * norm_w rounded to XDT, the values
 // sf_rmsnorm would have stored in an XDT buffer).
@@ -295,7 +306,7 @@ k_lm_head_argmax(const uint16_t *__restrict__ w, const void *__restrict__ x,
     __hip_atomic_store((uint32_t *)(part_val + blockIdx.x), sf_bitcast<uint32_t>(b),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(part_idx + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the partial is stored before the count
+    __builtin_amdgcn_s_waitcnt(0);  // the partial is stored before the count (see above)
     const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == gridDim.x - 1;
   }
@@ -453,7 +464,7 @@ k_lm_head_rows(const uint16_t *__restrict__ w, const void *__restrict__ x,
     __hip_atomic_store(part_idx + (size_t)tid * gridDim.x + blockIdx.x, bi, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count
+  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count (ordering argument above k_lm_head_argmax)
   __syncthreads();
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -620,7 +631,7 @@ k_lm_head_rows_mfma(const uint16_t *__restrict__ w, const void *__restrict__ x,
     __hip_atomic_store(part_idx + (size_t)tid * gridDim.x + blockIdx.x, bi, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count
+  __builtin_amdgcn_s_waitcnt(0);  // the partials are stored before the count (ordering argument above k_lm_head_argmax)
   __syncthreads();
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
