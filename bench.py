@@ -1128,8 +1128,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.sweep_attn_splits:
         d = args.sweep_attn_splits
-        Ts = (128, 512, 1024, 4096, 16384) if d <= 64 else (256, 320, 448, 512, 1024, 4096)
-        print(json.dumps(sweep_attn_splits(dev, d, Ts)))
+        Ts = (128, 512, 1024, 2048, 4096, 8192, 16384) if d <= 64 else (256, 512, 2048, 4096, 8192, 16384)
+        print(json.dumps(sweep_attn_splits(dev, d, Ts, splits=(1, 8, 16, 32, 64, 128))))
         return 0
     if args.profile_case:
         st = torch.cuda.Stream(dev)

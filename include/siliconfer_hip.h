@@ -201,7 +201,7 @@ int sf_kv_quant_append(const void *k_new, const void *v_new, int in_dtype, int8_
 size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits);
 /* Default split count (the reference's _choose_n_tiles, q4_attention.py:183-197,
  * re-tuned for MI355X): one split up to 160 cached tokens, then 32 tokens per
- * split up to 1024 tokens and 64 above, 8 to 64 splits (any head_dim).
+ * split up to 2048 tokens and 64 above, 8 to 128 splits (any head_dim).
  * sf_attn_default_splits is the same rule. */
 int sf_attn_default_splits(int B, int KVH, int T);
 int sf_attn_default_splits_d(int B, int KVH, int T, int D);

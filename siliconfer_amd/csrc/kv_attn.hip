@@ -1034,7 +1034,13 @@ k_attn_merge(const float *__restrict__ acc, const float *__restrict__ ml, void *
   // every argument fetched in one round at entry (the compiler would split them)
   asm volatile("" ::"s"(acc), "s"(ml), "s"(out), "s"(odt), "s"(rows), "s"(D), "s"(S));
   const int P = sf_merge_span(S), GS = P / SPL;
-  const int e = blockIdx.x * (kMergeThreads / GS) + threadIdx.x / GS, g = threadIdx.x % GS;
+  // workgroup i runs on XCD i % 8: the blocks of outputs are dealt so that
+  // each XCD takes one contiguous eighth of them (its L2 then fetches only the
+  // partials of those heads, not every head's)
+  const int nb = gridDim.x, per_x = (nb + 7) >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int full = nb - 8 * (per_x - 1);  // XCDs that take per_x blocks (the rest per_x - 1)
+  const int blk = xcd < full ? xcd * per_x + j : full * per_x + (xcd - full) * (per_x - 1) + j;
+  const int e = blk * (kMergeThreads / GS) + threadIdx.x / GS, g = threadIdx.x % GS;
   const int n = rows * D, ec = min(e, n - 1);  // lanes past the last output compute, then drop
   const int bh = ec / D, d = ec - bh * D;
   const float2_t *mlr = (const float2_t *)ml + (size_t)bh * S;
@@ -1082,23 +1088,25 @@ extern "C" size_t sf_attn_workspace_bytes(int B, int H, int D, int n_splits) {
 
 extern "C" int sf_attn_default_splits_d(int B, int KVH, int T, int D) {
   // One split (one workgroup per (b, kv head), no merge launch) up to 160
-  // tokens; beyond, 32 tokens per split up to 1024 cached tokens and 64 above,
-  // at least 8 and at most 64 splits. Measured on MI355X at 14 / 2 heads,
-  // graph-timed over cold caches (us, one split / the rule's count):
-  //   head_dim 64:  T = 128: 4.8 / 4.9;  256: 5.4 / 5.2 (8);  512: 6.4 / 5.6 (16);
-  //                 1024: 8.5 / 5.9 (32);  4096: 6.4 (64; 32: 6.6);  16384: 7.9 (64);
-  //   head_dim 128: T = 128: 5.6 / 5.9;  256: 6.7 / 6.1 (8);  512: 9.2 / 6.4 (16);
-  //                 2048: 20.8 / 7.1 (32);  4096: 7.9 (64).
+  // tokens; beyond, 32 tokens per split up to 2048 cached tokens and 64 above,
+  // 8 to 128 splits. Measured on MI355X at 14 / 2 heads, graph-timed over cold
+  // caches (us at the rule's count, other counts in parentheses):
+  //   head_dim 64:  T = 128: 4.8 (1);  512: 5.6 (16; 1: 6.4);  1024: 5.7 (32; 64:
+  //                 5.8);  2048: 5.8 (64; 32: 5.9);  4096: 6.2 (64; 128: 6.2, 32:
+  //                 6.5);  8192: 6.7 (128; 64: 6.8);  16384: 7.4 (128; 64: 7.6);
+  //   head_dim 128: T = 512: 6.4 (16; 1: 9.2);  2048: 6.8 (64; 32: 6.9);  4096:
+  //                 7.4 (64; 128: 7.5);  8192: 8.2 (128; 64: 8.3);  16384: 9.3
+  //                 (128; 64: 10.1).
   // Eight waves per split workgroup (one tile each) instead of four measured
   // no faster at 4096-16384 tokens.
   (void)B;
   (void)KVH;
   (void)D;
   if (T <= 160) return 1;
-  const int tps = T <= 1024 ? 32 : 64;
+  const int tps = T <= 2048 ? 32 : 64;
   int s = (T + tps - 1) / tps;
   if (s < 8) s = 8;
-  if (s > 64) s = 64;
+  if (s > 128) s = 128;
   return s;
 }
 

@@ -152,15 +152,16 @@ def test_attention_validation_and_sizes():
     rc = lib.sf_attn_decode_i8kv(None, 0, None, None, None, None, 1, None, 0, None, 0,
                                  1, 14, 3, 16, 16, 64, 0.1, 1, None)
     assert rc == -1 and "not a multiple" in _lib.last_error()
-    assert lib.sf_attn_default_splits(1, 2, 16384) == 64
+    assert lib.sf_attn_default_splits(1, 2, 16384) == 128
     assert lib.sf_attn_default_splits(1, 2, 4096) == 64
     assert lib.sf_attn_default_splits(1, 2, 100) == 1
     assert lib.sf_attn_default_splits(1, 2, 160) == 1 and lib.sf_attn_default_splits(1, 2, 161) == 8
     assert lib.sf_attn_default_splits_d(1, 2, 512, 64) == 16
     assert lib.sf_attn_default_splits_d(1, 2, 1024, 128) == 32
-    assert lib.sf_attn_default_splits_d(1, 2, 1025, 128) == 17
-    assert lib.sf_attn_default_splits_d(1, 2, 2048, 64) == 32
+    assert lib.sf_attn_default_splits_d(1, 2, 2048, 64) == 64
+    assert lib.sf_attn_default_splits_d(1, 2, 2049, 64) == 33
     assert lib.sf_attn_default_splits_d(1, 2, 4096, 128) == 64
+    assert lib.sf_attn_default_splits_d(1, 2, 8192, 128) == 128
 
 
 def test_kv_append_validation():

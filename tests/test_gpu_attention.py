@@ -277,10 +277,12 @@ def test_one_split_head_dim_128(dev, H, T):
           what=f"D=128 H={H} one split fp16 scales T={T}")
 
 
-@pytest.mark.parametrize("D,T", [(64, 160), (64, 161), (128, 160), (128, 161), (64, 1024), (64, 1025)])
+@pytest.mark.parametrize("D,T", [(64, 160), (64, 161), (128, 160), (128, 161), (64, 2048), (64, 2049),
+                                 (64, 16384), (128, 8192)])
 def test_default_split_switch(dev, D, T):
     """The default split count on either side of the one-split limit and of
-    the 32 -> 64 tokens-per-split step, through attention_decode's own pick
+    the 32 -> 64 tokens-per-split step, and at 128 splits (a merge span of two
+    splits per lane), through attention_decode's own pick
     (fp32 and fp16 scales); default_splits reports the count it uses."""
     assert (default_splits(1, 2, T, D) == 1) == (T <= 160)
     for sdt in (np.float32, np.float16):

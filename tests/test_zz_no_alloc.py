@@ -36,7 +36,7 @@ def _run(dev, lib, noalloc, q, kc, ks, vc, vs, n_splits):
                                              vcd.data_ptr(), vsd.data_ptr(), F16, out.data_ptr(), F32,
                                              B, H, KVH, T, T, D, D ** -0.5, n_splits, st)
     else:
-        nb = lib.sf_attn_workspace_bytes(B, H, D, max(n_splits, 1) if n_splits else 64)
+        nb = lib.sf_attn_workspace_bytes(B, H, D, n_splits or lib.sf_attn_default_splits_d(B, KVH, T, D))
         ws = torch.zeros(max(nb, 1 << 16), dtype=torch.uint8, device=dev)
         rc = lib.sf_attn_decode_i8kv(qd.data_ptr(), F16, kcd.data_ptr(), ksd.data_ptr(),
                                      vcd.data_ptr(), vsd.data_ptr(), F16, out.data_ptr(), F32,
