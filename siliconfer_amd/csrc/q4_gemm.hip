@@ -517,12 +517,18 @@ k_splitk_reduce(const float *__restrict__ part, void *__restrict__ Y, int ydt, f
 //    column block c (32 columns) of step s + 1 into the exact integers q - z
 //    as bf16 or fp16 MFMA B operands (lane order) in one of two LDS operand
 //    buffers, which the math waves read in step s + 1.
-// Each wave's loads per step are a fixed count (math wave w: X fragments
-// 4 (w / 2) + 2 (w % 2), + 1 and, for w < groups per step, that group's
-// scale row; convert wave 8 + c: W units 2 c, 2 c + 1 and, with zero-points
-// and c < groups per step, that group's zero-point row), so each wait is an
-// exact s_waitcnt vmcnt: a math wave waits for its loads of step s at the top
-// of step s, a convert wave for its loads of step s + 1.
+// The math waves issue every load, in a fixed order per step: math wave w
+// loads W unit w, then, for w < groups per step, that group's scale row or,
+// with zero-points and groups per step <= w < 2 groups per step, zero-point
+// row w - groups per step, then X fragments 4 (w / 2) + 2 (w % 2), + 1. At the
+// top of step s a math wave waits (s_waitcnt vmcnt) until at most its X loads
+// of step s + 1 and its loads of step s + 2 are outstanding: its X of step s
+// and its W and scale / zero-point rows of step s + 1, which the convert
+// waves read during step s, have landed. The convert waves issue nothing and
+// only convert: with the W loads in the convert waves, each of them spent
+// about a third of its step waiting to issue its loads behind the math
+// waves' X loads (shader-clock stamps), and that wave set the step time;
+// moving them measured 8% faster at config 2.
 constexpr int G_BM = 128, G_BN = 128, G_BK = 64, G_STAGES = 4;
 constexpr int G_MATH = 8, G_THREADS = (G_MATH + 4) * 64;  // math waves, then 4 convert waves
 constexpr int G_XL = 16 / G_MATH;               // X fragments a math wave loads per step
@@ -560,18 +566,41 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     asm volatile("" ::: "memory");     \
   } while (0)
 
+// One byte of v, sign-extended, to fp32 (an SDWA source select: the byte's
+// extraction, sign extension and conversion in one instruction).
+#define SF_SBYTE_F32(out, v, B)                                                                   \
+  asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_" #B \
+      : "=v"(out)                                                                              \
+      : "v"(v))
+
 // The bf16 B operand of 8 codes (one dword of a unit lane) as the exact
 // integers code - z: the dword's nibble i is k element 2 i (i < 4) or
 // 2 (i - 4) + 1, the pairs the GEMV's dequantization forms
-// ((d >> 4 i) & 0x000F000F); each byte converts to fp32 exactly, and
-// code - z (|.| <= 15) is exact in bf16.
-__device__ __forceinline__ u32x4 dequant_bf16_exact(uint32_t d, float zf) {
-  const uint32_t e = d & 0x0F0F0F0Fu, o = (d >> 4) & 0x0F0F0F0Fu;  // nibbles 0,2,4,6 / 1,3,5,7
-  auto pk = [&](uint32_t v, int b0, int b1) {
-    const float2_t f = {(float)((v >> (8 * b0)) & 0xFFu) - zf, (float)((v >> (8 * b1)) & 0xFFu) - zf};
+// ((d >> 4 i) & 0x000F000F). The nibbles of each half go one per byte, and
+// ((b ^ 0x80) - z) ^ 0x80 turns byte b into the two's complement int8 of
+// b - z with no borrow between bytes (0x80 + b - z stays in 0x71..0x8F), so
+// each byte converts to fp32 exactly in one instruction; code - z
+// (|.| <= 15) is exact in bf16. 19 VALU instructions per 8 codes, against 28
+// for the same values through per-nibble extracts, integer subtracts and
+// conversions.
+__device__ __forceinline__ u32x4 dequant_bf16_exact(uint32_t d, uint32_t z) {
+  const uint32_t zz = z * 0x01010101u;
+  const uint32_t e = (((d & 0x0F0F0F0Fu) ^ 0x80808080u) - zz) ^ 0x80808080u;         // nibbles 0,2,4,6
+  const uint32_t o = ((((d >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u) - zz) ^ 0x80808080u;  // nibbles 1,3,5,7
+  float e0, e1, e2, e3, o0, o1, o2, o3;
+  SF_SBYTE_F32(e0, e, 0);
+  SF_SBYTE_F32(e1, e, 1);
+  SF_SBYTE_F32(e2, e, 2);
+  SF_SBYTE_F32(e3, e, 3);
+  SF_SBYTE_F32(o0, o, 0);
+  SF_SBYTE_F32(o1, o, 1);
+  SF_SBYTE_F32(o2, o, 2);
+  SF_SBYTE_F32(o3, o, 3);
+  auto pk = [](float a, float b) {
+    const float2_t f = {a, b};
     return sf_bitcast<uint32_t>(__builtin_convertvector(f, bf16x2_t));
   };
-  return u32x4{pk(e, 0, 2), pk(o, 0, 2), pk(e, 1, 3), pk(o, 1, 3)};
+  return u32x4{pk(e0, e2), pk(o0, o2), pk(e1, e3), pk(o1, o3)};
 }
 
 template <int XDT, bool ASYM, int GK>
@@ -607,40 +636,38 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // math wave cw loads row block cw / 2's fragments G_XL (cw % 2) ..
   const int mrow = m0 + (cw >> 1) * 32 + l32;
   const bool mrow_ok = mrow < M;
-  const bool extra = math ? cw < NG : (ASYM && cw < NG);
+  // a scale row (math waves 0 .. NG - 1) or a zero-point row (NG .. 2 NG - 1)
+  const bool extra = math && (cw < NG || (ASYM && cw < 2 * NG));
   const int cell = min((n0 >> 3) + (lane & 15), ncells - 1);  // lanes 16.. repeat lane 15's row
   auto issue = [&](int step) {
     const int sc = min(step, s1 - 1);
     uint8_t *stage = smem + (step & 3) * SB;
-    if (math) {
-#pragma unroll
-      for (int i = 0; i < G_XL; ++i) {
-        const int f = G_XL * (cw & 1) + i;
-        const int k = sc * G_BK + f * 16 + 8 * h;
-        // past the resource (reads zero) unless in range; a select, not a branch
-        const uint32_t in = ((uint32_t)mrow * (uint32_t)K + (uint32_t)k) * 2u;
-        const uint32_t keep = 0u - (uint32_t)(mrow_ok && k < K);
-        const uint32_t off = (in & keep) | (0x80000000u & ~keep);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (4 * (cw >> 1) + f) * G_FRAG), 16,
-                                                 off, 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int wtile = min((n0 >> 4) + 2 * cw + u, ntiles - 1);
-        const uint8_t *unit = wq + ((size_t)wtile * nblk + (sc >> 1)) * 1024 + lane * 16;
-        __builtin_amdgcn_global_load_lds((gbl_void *)unit,
-                                         (lds_void *)(stage + G_W_OFF + (2 * cw + u) * 1024), 16, 0, 0);
-      }
+    if (!math) return;
+    {
+      const int wtile = min((n0 >> 4) + cw, ntiles - 1);
+      const uint8_t *unit = wq + ((size_t)wtile * nblk + (sc >> 1)) * 1024 + lane * 16;
+      __builtin_amdgcn_global_load_lds((gbl_void *)unit, (lds_void *)(stage + G_W_OFF + cw * 1024), 16, 0, 0);
     }
     if (extra) {
-      const int gi = min(GK == 0 ? 2 * sc + cw : GK == 1 ? sc : sc / spg, G - 1);
+      const int q = cw < NG ? cw : cw - NG;  // the group of the step whose row this wave loads
+      const int gi = min(GK == 0 ? 2 * sc + q : GK == 1 ? sc : sc / spg, G - 1);
       const size_t c = (size_t)cell * G + gi;
-      if (math)
-        __builtin_amdgcn_global_load_lds((gbl_void *)(st + c * 8), (lds_void *)(stage + G_S_OFF + cw * 1024),
+      if (cw < NG)
+        __builtin_amdgcn_global_load_lds((gbl_void *)(st + c * 8), (lds_void *)(stage + G_S_OFF + q * 1024),
                                          16, 0, 0);
       else
-        __builtin_amdgcn_global_load_lds((gbl_void *)(zt + c * 4), (lds_void *)(stage + ZO + cw * 256), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((gbl_void *)(zt + c * 4), (lds_void *)(stage + ZO + q * 256), 4, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < G_XL; ++i) {
+      const int f = G_XL * (cw & 1) + i;
+      const int k = sc * G_BK + f * 16 + 8 * h;
+      // past the resource (reads zero) unless in range; a select, not a branch
+      const uint32_t in = ((uint32_t)mrow * (uint32_t)K + (uint32_t)k) * 2u;
+      const uint32_t keep = 0u - (uint32_t)(mrow_ok && k < K);
+      const uint32_t off = (in & keep) | (0x80000000u & ~keep);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(stage + (4 * (cw >> 1) + f) * G_FRAG), 16,
+                                               off, 0, 0, 0);
     }
   };
 
@@ -664,7 +691,7 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const uint32_t zq = z[GK == 0 ? kk >> 1 : 0];
-      const u32x4 b = BF ? dequant_bf16_exact(d[kk], (float)zq) : sf_gemv::dequant_f16(d[kk], zq, dk);
+      const u32x4 b = BF ? dequant_bf16_exact(d[kk], zq) : sf_gemv::dequant_f16(d[kk], zq, dk);
       *(u32x4 *)(bo + (cw * 4 + kk) * 1024 + lane * 16) = b;
     }
   };
@@ -784,17 +811,18 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
   // Pipeline. Loads of step s go out during step s - 3 (the first three in
   // the prologue) into the stage step s - 4 used; after the barrier at the top
   // of step s every wave is done with step s - 1's stage and operand buffer
-  // (s + 1) % 2, every math wave's loads of step s and every convert wave's
-  // loads of step s + 1 have landed, and operand buffer s % 2 holds step s's
-  // operands. Nothing the compiler loads into registers goes to global memory
-  // inside the loop, so these loads are the only vector-memory counts.
+  // (s + 1) % 2, the X of step s and the W, scale and zero-point rows of step
+  // s + 1 have landed, and operand buffer s % 2 holds step s's operands.
+  // Nothing the compiler loads into registers goes to global memory inside
+  // the loop, so these loads are the only vector-memory counts. A math wave
+  // issues L = 1 + extra + G_XL loads per step.
   if (s0 < s1) {
     issue(s0);
     issue(s0 + 1);
     issue(s0 + 2);
-    if (!math) {  // this wave's loads of step s0 (two later steps' may remain)
-      if (extra) SF_WAIT_VM(6);
-      else SF_WAIT_VM(4);
+    if (math) {  // W and the scale / zero-point row of step s0 (its X and two later steps' may remain)
+      if (extra) SF_WAIT_VM(G_XL + 2 * (G_XL + 2));
+      else SF_WAIT_VM(G_XL + 2 * (G_XL + 1));
     }
     SF_BARRIER();
     if (!math) convert(s0);
@@ -803,18 +831,14 @@ k_q4_gemm_ws(const uint8_t *__restrict__ wq, const f16 *__restrict__ st,
       for (int u = 0; u < 4; ++u) {
         const int step = s + u;
         if (step >= s1) break;
-        if (math) {
-          if (extra) SF_WAIT_VM(2 * (G_XL + 1));
-          else SF_WAIT_VM(2 * G_XL);
-        } else {
-          if (extra) SF_WAIT_VM(3);
-          else SF_WAIT_VM(2);
+        if (math) {  // X of step s, W and rows of step s + 1 (X of s + 1 and step s + 2's may remain)
+          if (extra) SF_WAIT_VM(G_XL + G_XL + 2);
+          else SF_WAIT_VM(G_XL + G_XL + 1);
         }
         SF_BARRIER();
         if (math) {
           math_step(step, [&] { issue(step + 3); });
         } else {
-          issue(step + 3);
           if (step + 1 < s1) convert(step + 1);
         }
       }
