@@ -19,6 +19,7 @@ from siliconfer_amd import _lib
 from siliconfer_amd.kernels import Q4Weight
 
 pytestmark = pytest.mark.gpu
+SF_EUNSUPPORTED = -2  # include/siliconfer_hip.h
 F32, F16, BF16 = _lib.SF_F32, _lib.SF_F16, _lib.SF_BF16
 ACTS = [torch.float16, torch.bfloat16, torch.float32]
 
@@ -201,10 +202,12 @@ ROW_SHAPES = [(1152, 896, 64, False), (9728, 896, 64, True), (896, 4864, 64, Fal
 @pytest.mark.parametrize("op", [_lib.SF_PRE_RMSNORM, _lib.SF_PRE_SILU_MUL])
 def test_fused_rows_equal_separate_kernels(dev, B, N, K, g, asym, op):
     """sf_q4_gemv_fused_rows == sf_rmsnorm / sf_silu_mul then sf_q4_gemv, bit
-    for bit, with an [N] bias and with the per-row residual (bias = y_f32)."""
+    for bit, with an [N] bias and with the per-row residual (bias = y_f32).
+    Where the folded kernels have no plan for the shape, the entry point
+    refuses it with SF_EUNSUPPORTED before launching anything, and the
+    separate kernels that callers run instead meet the oracle."""
     lib = _lib.load()
-    if not lib.sf_q4_gemv_fused_rows_supported(op, B, N, K, g, int(asym), F16):
-        pytest.skip("plan outside the folded kernels' range (separate kernels run instead)")
+    supported = bool(lib.sf_q4_gemv_fused_rows_supported(op, B, N, K, g, int(asym), F16))
     w, pk, s, z = make_weight(dev, N, K, g, asym, N + K + B)
     rng = np.random.default_rng(N * B + op)
     rms = op == _lib.SF_PRE_RMSNORM
@@ -220,6 +223,18 @@ def test_fused_rows_equal_separate_kernels(dev, B, N, K, g, asym, op):
     ref = torch.empty((B, N), device=dev)
     got = torch.empty((B, N), device=dev)
     gemv_rows(lib, w, xn, ref, bias)
+    if not supported:
+        sentinel = torch.full((B, N), 7.0, device=dev)
+        rc = lib.sf_q4_gemv_fused_rows(
+            w.blob.data_ptr(), src.data_ptr(), op, None if nw is None else nw.data_ptr(), 1e-6, F16, None,
+            F32, sentinel.data_ptr(), bias.data_ptr(), F32, B, N, K, g, int(asym), st())
+        torch.cuda.synchronize()
+        assert rc == SF_EUNSUPPORTED and "LDS staging" in _lib.last_error(), (rc, _lib.last_error())
+        assert bool((sentinel == 7.0).all()), "a refused call wrote its output"
+        exp = linear.gemv(pk, s.astype(np.float16).astype(np.float64),
+                          xn.float().cpu().numpy().astype(np.float64), g, zeros=z) + bias.cpu().numpy()
+        linear.assert_close(ref.cpu().numpy(), exp, 1e-3, f"separate kernels op={op} B={B}")
+        return
     fused_rows(lib, w, src, op, nw, B, got, bias)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
