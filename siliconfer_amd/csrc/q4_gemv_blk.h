@@ -292,6 +292,15 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   // scale slots or the sums of the bf16 path need the room)
   constexpr int XR = XL ? 1 : BPW <= 2 ? BPW : (ASYM || BFP || GK != 0) ? 2 : 3;
   constexpr int XPRE = XL ? 0 : (XR == BPW ? BPW : XR - 1);
+  // Direct loads with every unit's activations loaded up front: a unit takes
+  // two loads instead of four. The A operand has 16 rows and only rows < B
+  // (B <= 8) are ever stored, so lane row nl loads fragment 2 p + nl / 8 of
+  // batch row nl % 8 (p = 0, 1), and a DPP row rotate by 8 hands rows 0..7 the
+  // fragments rows 8..15 loaded (the same operand values in every stored row:
+  // the same bits). With the loads in a ring (issued just before use) the
+  // rotate's latency sits in front of the MFMAs and measured slower, so the
+  // ring keeps four loads.
+  constexpr bool X2 = !XL && XR == BPW;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float inv_s[8];
   // Every argument the prologue reads, fetched in one round at entry: left to
@@ -406,7 +415,8 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   u32x4 xs[XR][4];
   if constexpr (!XL) {
     xrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, 0, B * K * 2, 0x00020000);
-    xoff = nl < B ? (nl * K + 8 * kg) * 2 : 0x40000000;
+    const int xrow = X2 ? nl & 7 : nl;
+    xoff = xrow < B ? (xrow * K + 8 * kg) * 2 : 0x40000000;
   }
   const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
@@ -425,8 +435,9 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
     if constexpr (!XL) {
       const int kb = min(cb + i, blast) * kUnitK;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int o = kb + 32 * j + 8 * kg < K ? xoff + (kb + 32 * j) * 2 : 0x40000000;
+      for (int j = 0; j < (X2 ? 2 : 4); ++j) {
+        const int jj = X2 ? 2 * j + (nl >> 3) : j;  // the fragment this lane fetches
+        const int o = kb + 32 * jj + 8 * kg < K ? xoff + (kb + 32 * jj) * 2 : 0x40000000;
         xs[i % XR][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, o, 0, 0);
       }
     }
@@ -560,10 +571,23 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
       if (i + XPRE < BPW) xload(i + XPRE);
     const int kb = min(cb + i, blast) * kUnitK;
     u32x4 av[4];
+    if constexpr (X2) {
+      auto from_row8 = [](const u32x4 &v) {  // each lane takes the value of lane + 8 of its row
+        u32x4 r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (XL) av[j] = *(const u32x4 *)(xl + (size_t)arow * a.xp + kb + 32 * j + 8 * kg);
-      else av[j] = xs[i % XR][j];
+        for (int d = 0; d < 4; ++d) r[d] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[d], 0x128, 0xF, 0xF, false);
+        return r;
+      };
+      av[0] = xs[i % XR][0];
+      av[1] = from_row8(xs[i % XR][0]);
+      av[2] = xs[i % XR][1];
+      av[3] = from_row8(xs[i % XR][1]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (XL) av[j] = *(const u32x4 *)(xl + (size_t)arow * a.xp + kb + 32 * j + 8 * kg);
+        else av[j] = xs[i % XR][j];
+      }
     }
     // bf16 path: sum(x) of each slot's k (rows m = 4 kg + r of the lane)
     float4_t xsum[GS::SLOTS];
