@@ -290,17 +290,20 @@ k_q4_gemv_blk(BlkArgs a, SfRopeAppend rope, const int *__restrict__ pos_dev) {
   constexpr bool BFP = XDT != SF_F16;                 // bf16 MFMA path (offset via sum(x))
   // direct mode: units of x held in registers (fewer when zero-points, several
   // scale slots or the sums of the bf16 path need the room)
-  constexpr int XR = XL ? 1 : BPW <= 2 ? BPW : (ASYM || BFP || GK != 0) ? 2 : 3;
+  //
+  // A unit's activations take two direct loads, not four. The A operand has 16
+  // rows and only rows < B (B <= 8) are ever stored, so lane row nl loads
+  // fragment 2 p + nl / 8 of batch row nl % 8 (p = 0, 1), and a DPP row rotate
+  // by 8 hands rows 0..7 the fragments rows 8..15 loaded (the same operand
+  // values in every stored row: the same bits). A ring slot then holds half
+  // the registers, so the ring is twice as deep as the four-load one was
+  // (with the four-load depth the rotate's latency sat in front of the MFMAs
+  // and measured slower at K = 11008; twice as deep, 4-5% faster there at
+  // batch 3-8, and 0.3-0.4 us faster at K = 4096, batch 5-8).
+  constexpr int XR4 = BPW <= 2 ? BPW : (ASYM || BFP || GK != 0) ? 2 : 3;  // the four-load depth
+  constexpr int XR = XL ? 1 : (2 * XR4 < BPW ? 2 * XR4 : BPW);
   constexpr int XPRE = XL ? 0 : (XR == BPW ? BPW : XR - 1);
-  // Direct loads with every unit's activations loaded up front: a unit takes
-  // two loads instead of four. The A operand has 16 rows and only rows < B
-  // (B <= 8) are ever stored, so lane row nl loads fragment 2 p + nl / 8 of
-  // batch row nl % 8 (p = 0, 1), and a DPP row rotate by 8 hands rows 0..7 the
-  // fragments rows 8..15 loaded (the same operand values in every stored row:
-  // the same bits). With the loads in a ring (issued just before use) the
-  // rotate's latency sits in front of the MFMAs and measured slower, so the
-  // ring keeps four loads.
-  constexpr bool X2 = !XL && XR == BPW;
+  constexpr bool X2 = !XL;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float inv_s[8];
   // Every argument the prologue reads, fetched in one round at entry: left to
