@@ -113,6 +113,17 @@ class QuantizedKVCache:
         return 2 * B * KVH * self._len * (D + es)
 
     # -- device-resident fast path -------------------------------------------
+    def reserve(self, B: int, KVH: int, D: int, need: int, device) -> None:
+        """Make the buffers hold at least `need` positions of [B, KVH, *, D]
+        (allocating them on first use) without appending anything."""
+        self._ensure(torch.empty((B, KVH, 0, D), device=device), need)
+
+    def set_length(self, n: int) -> None:
+        """Mark the first n positions valid (a kernel wrote them in place)."""
+        if self._qk is None or not 0 <= n <= self._qk.shape[2]:
+            raise SFError(f"length {n} outside the cache's buffers")
+        self._len = int(n)
+
     def _ensure(self, k: torch.Tensor, need: int) -> None:
         B, KVH, _, D = k.shape
         if self._qk is not None:
