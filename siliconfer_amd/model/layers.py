@@ -87,6 +87,16 @@ def apply_rope(x: torch.Tensor, offset: int, freqs: torch.Tensor) -> torch.Tenso
     return (xf * c + rot * s).to(x.dtype)
 
 
+def _host(a) -> np.ndarray:
+    """A checkpoint array (numpy, or a torch tensor on any device) as numpy."""
+    return a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+
+
+def _f32(a) -> torch.Tensor:
+    """A checkpoint array as an fp32 torch tensor (on its own device)."""
+    return a.detach().float() if isinstance(a, torch.Tensor) else torch.from_numpy(np.asarray(a, np.float32))
+
+
 def _dense(in_f: int, out_f: int, bias: bool, device) -> torch.nn.Linear:
     return torch.nn.Linear(in_f, out_f, bias=bias, device=device, dtype=torch.float32)
 
@@ -266,18 +276,19 @@ class TransformerBlock(torch.nn.Module):
                 b = weights.get(p + ".bias")
                 if p + ".q4_packed" in weights:
                     z = weights.get(p + ".q4_zeros")
-                    lin = Q4Linear(weights[p + ".q4_packed"].numpy(), weights[p + ".q4_scales"].float().numpy(),
-                                   None if z is None else z.numpy(),
-                                   None if b is None else b.float(), group_size, device=dev)
+                    lin = Q4Linear(_host(weights[p + ".q4_packed"]),
+                                   _host(weights[p + ".q4_scales"]).astype(np.float32),
+                                   None if z is None else _host(z),
+                                   None if b is None else _f32(b), group_size, device=dev)
                 else:
-                    W = weights[p + ".weight"]
+                    W = _f32(weights[p + ".weight"])
                     lin = _dense(W.shape[1], W.shape[0], b is not None, dev)
                     with torch.no_grad():
-                        lin.weight.copy_(W.float())
+                        lin.weight.copy_(W)
                         if b is not None:
-                            lin.bias.copy_(b.float())
+                            lin.bias.copy_(_f32(b))
                 setattr(mod, name, lin)
         with torch.no_grad():
-            blk.input_layernorm.weight.copy_(weights[f"{pre}.input_layernorm.weight"].float())
-            blk.post_attention_layernorm.weight.copy_(weights[f"{pre}.post_attention_layernorm.weight"].float())
+            blk.input_layernorm.weight.copy_(_f32(weights[f"{pre}.input_layernorm.weight"]))
+            blk.post_attention_layernorm.weight.copy_(_f32(weights[f"{pre}.post_attention_layernorm.weight"]))
         return blk

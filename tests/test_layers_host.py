@@ -35,3 +35,17 @@ def test_host_tensors_are_refused(which):
             "mlp": lambda: blk.mlp(x), "block": lambda: blk(x, None)}[which]
     with pytest.raises(SFError):
         call()
+
+
+def test_checkpoint_arrays_from_numpy_or_torch():
+    """from_weights reads checkpoint entries given as numpy arrays or torch tensors."""
+    import numpy as np
+
+    from siliconfer_amd.model.layers import _f32, _host
+
+    a = np.arange(6, dtype=np.uint8).reshape(2, 3)
+    assert np.array_equal(_host(a), a) and np.array_equal(_host(torch.from_numpy(a)), a)
+    h = np.array([1.5, -2.25], dtype=np.float16)
+    for src in (h, torch.from_numpy(h)):
+        t = _f32(src)
+        assert t.dtype == torch.float32 and t.tolist() == [1.5, -2.25]
