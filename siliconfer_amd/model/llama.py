@@ -197,8 +197,9 @@ class LlamaModel:
                     std: float = 0.02, max_prefill: int = 512, fuse: bool = True) -> "LlamaModel":
         """Random weights N(0, std) drawn on the device from `seed` (RMSNorm
         weights 1, q/k/v biases N(0, std) when the config has attention bias),
-        every projection RTN int4 symmetric with `group_size`, the tied
-        embedding in bf16."""
+        every projection RTN int4 symmetric with `group_size`, the embedding
+        in bf16, and a bf16 lm_head of its own drawn after the layers when the
+        config does not tie it to the embedding."""
         if not _lib.hip_available():
             raise SFError("no gfx950 HIP device: siliconfer_amd has no CPU fallback")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -227,7 +228,9 @@ class LlamaModel:
             ones = torch.ones(H, dtype=torch.float32, device=dev)
             layers.append(LayerWeights(qkv, bias, o, gate_up, down, ones, ones.clone()))
         norm_w = torch.ones(H, dtype=torch.float32, device=dev)
-        return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill, fuse)
+        head = None if c.tie_word_embeddings else randn(c.vocab_size, H).to(torch.bfloat16).contiguous()
+        return cls(config, layers, embed, norm_w, group_size, max_seq, act_dtype, max_prefill, fuse,
+                   lm_head=head)
 
     def export_weights(self, packed: bool = False) -> dict:
         """Host copies for a reference restatement: dequantized fp32 weights

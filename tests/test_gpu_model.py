@@ -17,7 +17,7 @@ import torch
 
 from oracle import model as OM
 from oracle.linear import assert_close
-from siliconfer_amd.model.config import ModelConfig, rope_tables
+from siliconfer_amd.model.config import ModelConfig, RoPEScalingConfig, rope_tables
 from siliconfer_amd.model.llama import LlamaModel, pack_sym_device
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +64,35 @@ def test_small_model_matches_oracle(dev, act):
     ids = np.random.default_rng(12).integers(0, SMALL.vocab_size, 13)
     tol = 2e-3 if act == torch.float32 else 1e-2
     check_against_oracle(m, SMALL, ids, 6, tol, f"small/{act}")
+
+
+GEOMETRIES = {
+    # Llama-style: head_dim 128, one kv head per 4 query heads, no qkv bias, an
+    # lm_head of its own, llama3 RoPE scaling
+    "llama_hd128": ModelConfig(hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                               num_attention_heads=4, num_key_value_heads=1, head_dim=128,
+                               vocab_size=1000, rms_norm_eps=1e-5, rope_theta=5e5,
+                               rope_scaling=RoPEScalingConfig("llama3", 8.0, 1.0, 4.0, 64),
+                               tie_word_embeddings=False, attention_bias=False),
+    # multi-head attention (a kv head per query head) at head_dim 64
+    "mha_hd64": ModelConfig(hidden_size=256, intermediate_size=640, num_hidden_layers=2,
+                            num_attention_heads=4, num_key_value_heads=4, head_dim=64,
+                            vocab_size=1000, rms_norm_eps=1e-6, rope_theta=1e6,
+                            tie_word_embeddings=True, attention_bias=True),
+}
+
+
+@pytest.mark.parametrize("geom", sorted(GEOMETRIES))
+@pytest.mark.parametrize("act", [torch.float32, torch.float16])
+def test_other_geometries_match_oracle(dev, geom, act):
+    """The decoder is not specialised to config 5's shape: head_dim 128 with GQA
+    4:1, untied lm_head and llama3 RoPE scaling, and MHA at head_dim 64, each
+    through a 21-token prompt (the GEMM) and 8 decode steps against the oracle."""
+    cfg = GEOMETRIES[geom]
+    m = LlamaModel.random_init(cfg, seed=21, group_size=64, device=dev, max_seq=64, act_dtype=act)
+    ids = np.random.default_rng(22).integers(0, cfg.vocab_size, 21)
+    tol = 2e-3 if act == torch.float32 else 1e-2
+    check_against_oracle(m, cfg, ids, 8, tol, f"{geom}/{act}")
 
 
 def test_prefill_in_chunks_equals_one_prefill(dev):
