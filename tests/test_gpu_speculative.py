@@ -154,6 +154,39 @@ def test_verify_rows_match_decode_and_oracle(dev, act, B):
             assert near_tie(ref[r], toks[r], OM.greedy(ref[r]), tol), f"row {r}: token"
 
 
+LLAMA_HD128 = ModelConfig(hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                          num_attention_heads=4, num_key_value_heads=1, head_dim=128, vocab_size=1000,
+                          rms_norm_eps=1e-5, rope_theta=5e5, tie_word_embeddings=False,
+                          attention_bias=False)
+
+
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B", [3, 8])
+def test_verify_rows_head_dim_128_match_oracle(dev, act, B):
+    """Verify rows at head_dim 128 with GQA 4:1 and an untied lm_head against
+    the oracle (the causal attention over the new rows and the batch GEMV at
+    these shapes), bf16 activations included."""
+    cfg = LLAMA_HD128
+    m = LlamaModel.random_init(cfg, seed=47, group_size=64, device=dev, max_seq=64, act_dtype=act)
+    tol = 1e-2 if act == torch.float16 else 3e-2
+    rng = np.random.default_rng(48 + B)
+    prompt = rng.integers(0, cfg.vocab_size, 13)
+    feed = rng.integers(0, cfg.vocab_size, B)
+    m.reset()
+    m.prefill(prompt)
+    toks = m.verify(feed, want_logits=True)
+    W = m.export_weights()
+    cos, sin = rope_tables(cfg, m.max_seq)
+    cache = OM.KVCache(cfg.num_hidden_layers)
+    OM.forward(W, cfg, prompt, cache, cos, sin)
+    ref = OM.forward(W, cfg, feed, cache, cos, sin)
+    for r in range(B):
+        got = m.vlogits[r].cpu().numpy()
+        assert_close(got, ref[r], tol, f"verify row {r} vs oracle")
+        if toks[r] != OM.greedy(ref[r]):
+            assert near_tie(ref[r], toks[r], OM.greedy(ref[r]), tol), f"row {r}: token"
+
+
 @pytest.mark.parametrize("max_seq,prompt_len", [(64, 9), (2048, 1100)])
 def test_verify_graph_equals_eager(dev, max_seq, prompt_len):
     """verify() replayed from its graph (positions read on the device) gives
