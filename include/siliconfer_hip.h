@@ -149,7 +149,10 @@ int sf_q4_gemv_fused_rope(const void *blob, const float *h, const float *norm_w,
  * q4_gemm_asym (bindings.cpp:98-150; q4_gemm.cpp:12-51). bf16/f16 MFMA on
  * integer-valued int4 codes, fp32 per-(row, group) scale epilogue; group sizes
  * that are not a multiple of 32 run on the VALU kernel sf_q4_gemv uses for them.
- * workspace: sf_q4_gemm_workspace_bytes(...) bytes (may be 0 -> NULL ok). */
+ * Up to 16 rows the call runs as sf_q4_gemv over 8-row slices (the same bits
+ * as those calls; the reference's GEMM is a loop of GEMVs too), unless y_f32
+ * doubles as the bias. workspace: sf_q4_gemm_workspace_bytes(...) bytes (may
+ * be 0 -> NULL ok). */
 size_t sf_q4_gemm_workspace_bytes(int M, int N, int K, int group_size);
 int sf_q4_gemm(const void *blob, const void *x, int x_dtype, void *y, int y_dtype, float *y_f32,
                const void *bias, int bias_dtype, int M, int N, int K, int group_size,

@@ -187,3 +187,46 @@ def test_gemm_partials_fold_into_rmsnorm(dev, N, K, has_zeros):
     ref = linear.gemm(pk, s16(s), X.float().cpu().numpy().astype(np.float64), 64,
                       zeros=z)
     linear.assert_close((x2 - h0).double().cpu().numpy(), ref, 1e-3, f"partials delta [{N},{K}]")
+
+
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M", [1, 5, 8, 9, 12, 16, 17])
+def test_few_rows_run_as_batch_gemvs(dev, xdtype, M):
+    """sf_q4_gemm at up to 16 rows runs as 8-row sf_q4_gemv slices: the same
+    bits as those calls (the bias and the fp32 copy included); 17 rows take the
+    tile kernel. Every case against the oracle."""
+    from siliconfer_amd import _lib
+
+    lib = _lib.load()
+    F16, F32 = _lib.SF_F16, _lib.SF_F32
+    rng = np.random.default_rng(300 + M)
+    N, K, g = 1000, 768, 64
+    pk, s, z = P.pack_weights_asym(rng.normal(0, 0.02, (N, K)).astype(np.float32), g)
+    w = Q4Weight(pk, s, z, g, device=dev)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    X = torch.as_tensor(rng.normal(0, 1, (M, K)).astype(np.float32)).to(dev).to(xdtype).contiguous()
+    b = torch.as_tensor(bias).to(dev)
+    wsb = lib.sf_q4_gemm_workspace_bytes(M, N, K, g)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    xd = _lib.dt(X)
+    Y = torch.full((M, N), 7.0, dtype=torch.float16, device=dev)
+    Y32 = torch.full((M, N), 7.0, dtype=torch.float32, device=dev)
+    _lib.check(lib.sf_q4_gemm(w.blob.data_ptr(), X.data_ptr(), xd, Y.data_ptr(), F16, Y32.data_ptr(),
+                              b.data_ptr(), F32, M, N, K, g, 1, ws.data_ptr() if wsb else None, wsb, st),
+               "sf_q4_gemm")
+    if M <= 16:
+        R = torch.empty_like(Y)
+        R32 = torch.empty_like(Y32)
+        for m0 in range(0, M, 8):
+            mb = min(8, M - m0)
+            _lib.check(lib.sf_q4_gemv(w.blob.data_ptr(), X[m0:].data_ptr(), xd, R[m0:].data_ptr(), F16,
+                                      R32[m0:].data_ptr(), b.data_ptr(), F32, mb, N, K, g, 1, st),
+                       "sf_q4_gemv")
+        torch.cuda.synchronize()
+        assert torch.equal(Y, R) and torch.equal(Y32, R32)
+    torch.cuda.synchronize()
+    xk = X.float().cpu().numpy().astype(np.float64)
+    ref = linear.gemm(pk, s16(s), xk, g, zeros=z) + bias[None, :]
+    linear.assert_close(Y32.cpu().numpy().astype(np.float64), ref, TOL, f"gemm M={M} {xdtype}")
+    linear.assert_close(Y.float().cpu().numpy().astype(np.float64), ref, TOL, f"gemm fp16 out M={M} {xdtype}")
