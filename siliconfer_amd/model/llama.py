@@ -35,6 +35,8 @@ from ..kernels.q4 import Q4Weight
 from .config import ModelConfig, rope_tables
 
 _DT = {torch.float32: _lib.SF_F32, torch.float16: _lib.SF_F16, torch.bfloat16: _lib.SF_BF16}
+# sf_q4_gemm runs up to this many rows as 8-row batch GEMVs (no K split)
+GEMM_GEMV_ROWS = 16
 
 
 def pack_sym_device(W: torch.Tensor, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -313,8 +315,8 @@ class LlamaModel:
         in the GEMM workspace (no reduce launch) and return their count; else
         launch nothing and return 0."""
         M = X.shape[0]
-        if self._gemv_ok(M, w):
-            return 0
+        if M <= GEMM_GEMV_ROWS and self._gemv_ok(min(M, 8), w):
+            return 0  # sf_q4_gemm runs these rows as 8-row batch GEMVs: no partials
         S = int(self.lib.sf_q4_gemm_splits(M, w.out_features, w.in_features, w.group_size))
         if S <= 1:
             return 0
