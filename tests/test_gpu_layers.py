@@ -3,9 +3,10 @@ reference's model/layers.py call surface) against the oracle of the
 reference's forward pass (oracle/model.py) on a tiny checkpoint.
 
 - A stack of TransformerBlocks with one QuantizedKVCache per layer (batch 1:
-  the fused RoPE + int8 append, causal prefill attention for the prompt, the
-  split-T decode attention per token) gives the oracle's logits at every step,
-  symmetric and asymmetric weights.
+  the fused RoPE + int8 append, causal prefill attention for the prompt and
+  for later chunks after the cached prefix, the split-T decode attention per
+  token) gives the oracle's logits at every step, symmetric and asymmetric
+  weights.
 - The reference's other cache forms take the device's fp32 route: no cache
   equals the oracle's blocks with unquantized K / V, a (k, v) tuple fed token
   by token equals one causal call, and batch 2 over an int8 cache equals the
@@ -69,6 +70,14 @@ def test_block_stack_int8_cache_matches_oracle(dev, tmp_path, sym):
         got.append(_logits(m, blocks, cfg, [t], caches))
         ref.append(OM.forward(W, cfg, [t], oc, cos, sin)[-1])
     assert caches[0].length() == 18 and caches[0].capacity >= 18
+    # prompt chunks after a cached prefix: 5 rows (the decode kernel's causal
+    # rows) and 17 rows (the flash prefill kernel), each from its offset
+    rng = np.random.default_rng(6)
+    for n in (5, 17):
+        chunk = rng.integers(0, cfg.vocab_size, n)
+        got.append(_logits(m, blocks, cfg, chunk, caches))
+        ref.append(OM.forward(W, cfg, chunk, oc, cos, sin)[-1])
+    assert caches[0].length() == 40
     for i, (g, r) in enumerate(zip(got, ref)):
         assert_close(g, r, 2e-3, f"sym={sym} step {i}")
 
