@@ -70,7 +70,9 @@ def test_config2_hqq_packed_prefill(dev, N, K):
                                      # groups of 96 (a group boundary inside a K step) and
                                      # 256 (four steps); split-K starting mid-group
                                      (130, 200, 288, 96), (70, 300, 1024, 256),
-                                     (64, 96, 1152, 128), (40, 50, 1152, 96)])
+                                     (64, 96, 1152, 128), (40, 50, 1152, 96),
+                                     # 7B / 8B MLP depths: K split over many 64-k steps
+                                     (96, 384, 14336, 128), (144, 136, 11008, 64)])
 def test_gemm_shapes_and_dtypes_sym(dev, xdtype, M, N, K, g):
     rng = np.random.default_rng(M + N + K)
     W = rng.normal(0, 1, (N, K)).astype(np.float32)
